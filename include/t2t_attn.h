@@ -1,0 +1,128 @@
+/*
+ * t2t_attn.h -- C ABI of libt2t_attn.so, the gfx950 masked flash-attention
+ * path (doc_causal / cross_doc_link) of tagseq2tagseq.
+ *
+ * Plain pointers and sizes only.  Every pointer argument is a device pointer
+ * unless stated otherwise; the caller owns all memory (the library allocates
+ * and frees nothing).  All work is enqueued on `stream` (a hipStream_t passed
+ * as void*; NULL = the null stream) with no host synchronisation.  Functions
+ * return T2T_OK (0) or a negative status; t2t_last_error() then returns a
+ * thread-local message.
+ *
+ * Mask model (the reference's mask_mod, model/graph_traversal/cross_doc_mask.py:348-357):
+ *   allowed(q, kv) = q >= kv && (doc[q] == doc[kv] ||
+ *                                OR_w (q_bits[w][q] & kv_bits[w][kv]) != 0)
+ * doc_causal (model/graph_traversal/block_mask_creator.py:121-129) is words == 0.
+ * Per-token inputs are laid out doc int32[Bm][T], q_bits / kv_bits
+ * uint64[Bm][words][T] (word-major, the reference's chunk list), with Bm = 1
+ * (one mask for every batch row, the reference's B=None) or Bm = B.
+ */
+#ifndef T2T_ATTN_H
+#define T2T_ATTN_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define T2T_OK 0
+#define T2T_EINVAL (-1)       /* bad pointer, size or stride */
+#define T2T_EUNSUPPORTED (-2) /* shape / dtype outside what the kernels implement */
+#define T2T_EHIP (-3)         /* a HIP launch or runtime call failed */
+
+#define T2T_DTYPE_BF16 0
+
+#define T2T_TILE 128   /* BlockMask tile edge (torch/nn/attention/flex_attention.py:395) */
+#define T2T_MAX_WORDS 8
+
+/* Tile classes in tile_class[]: matches torch's partial / full int8 grids
+ * (torch/nn/attention/flex_attention.py:1014-1018) folded into one byte. */
+#define T2T_TILE_SKIP 0
+#define T2T_TILE_PARTIAL 1
+#define T2T_TILE_FULL 2
+
+/* [B, H, T, D] tensor with unit stride along D; strides in elements. */
+typedef struct t2t_tensor {
+  void *data;
+  int64_t stride_b;
+  int64_t stride_h;
+  int64_t stride_t;
+} t2t_tensor;
+
+/* Mask inputs plus the eight BlockMask tables (nt = ceil(T / 128)):
+ * *_num int32[Bm][nt], *_idx int32[Bm][nt][nt].  Field meanings follow
+ * torch's BlockMask (kv_num_blocks, kv_indices, full_kv_num_blocks,
+ * full_kv_indices, q_num_blocks, q_indices, full_q_num_blocks, full_q_indices)
+ * with the head dimension dropped. */
+typedef struct t2t_mask {
+  const int32_t *doc;
+  const uint64_t *q_bits;
+  const uint64_t *kv_bits;
+  int32_t words;
+  int32_t mask_batch; /* Bm */
+  const int32_t *kv_num;
+  const int32_t *kv_idx;
+  const int32_t *full_kv_num;
+  const int32_t *full_kv_idx;
+  const int32_t *q_num;
+  const int32_t *q_idx;
+  const int32_t *full_q_num;
+  const int32_t *full_q_idx;
+} t2t_mask;
+
+/* Library version string (host memory, static). */
+const char *t2t_version(void);
+
+/* Thread-local message for the last non-OK status on this thread. */
+const char *t2t_last_error(void);
+
+/*
+ * Tile classification + ordered index lists of a BlockMask.
+ * Replaces create_block_mask(mask_mod, B=None, H=None, T, T)
+ * (torch/nn/attention/flex_attention.py:1144-1225) as called by
+ * create_doc_causal_block_mask (model/graph_traversal/block_mask_creator.py:132-139)
+ * and CrossDocLinkMaskCreator.__call__ (model/graph_traversal/cross_doc_mask.py:359-366),
+ * without materialising the [T, T] mask.
+ * Outputs: tile_class int8[Bm][nt][nt] and the eight tables of t2t_mask.
+ */
+int t2t_mask_meta(const int32_t *doc, const uint64_t *q_bits, const uint64_t *kv_bits,
+                  int32_t mask_batch, int32_t T, int32_t words, int8_t *tile_class,
+                  int32_t *kv_num, int32_t *kv_idx, int32_t *full_kv_num,
+                  int32_t *full_kv_idx, int32_t *q_num, int32_t *q_idx,
+                  int32_t *full_q_num, int32_t *full_q_idx, void *stream);
+
+/*
+ * Masked attention forward.  Replaces the flex_attention forward
+ * (torch/nn/attention/flex_attention.py:1396-1676; eager arithmetic
+ * torch/_higher_order_ops/flex_attention.py:202-267) that FlexSelfAttention
+ * calls from model/modules/layer.py:33.
+ * q [B,Hq,T,D], k/v [B,Hkv,T,D], o [B,Hq,T,D] (dtype), lse2 float[B][Hq][T]
+ * (contiguous) = log2-sum-exp2 of the masked row of (Q K^T * scale * log2 e);
+ * natural-log LSE = lse2 * ln 2; fully masked rows give o = 0, lse2 = -inf.
+ * Supported: dtype T2T_DTYPE_BF16, D in {64, 128}, Hq % Hkv == 0.
+ */
+int t2t_attn_fwd(const t2t_tensor *q, const t2t_tensor *k, const t2t_tensor *v,
+                 const t2t_tensor *o, float *lse2, int32_t B, int32_t Hq, int32_t Hkv,
+                 int32_t T, int32_t D, int32_t dtype, float scale, const t2t_mask *mask,
+                 void *stream);
+
+/*
+ * Masked attention backward.  Replaces flex_attention_backward as driven by
+ * FlexAttentionAutogradOp.backward (torch/_higher_order_ops/flex_attention.py:689-767;
+ * eager arithmetic sdpa_dense_backward :825-994).
+ * delta: float[B][Hq][T] workspace (overwritten).  dq like q; dk/dv like k/v
+ * (summed over each GQA group, written, not accumulated).  No atomics: the
+ * result is bitwise deterministic.
+ */
+int t2t_attn_bwd(const t2t_tensor *q, const t2t_tensor *k, const t2t_tensor *v,
+                 const t2t_tensor *o, const t2t_tensor *dout, const float *lse2,
+                 float *delta, const t2t_tensor *dq, const t2t_tensor *dk,
+                 const t2t_tensor *dv, int32_t B, int32_t Hq, int32_t Hkv, int32_t T,
+                 int32_t D, int32_t dtype, float scale, const t2t_mask *mask, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* T2T_ATTN_H */

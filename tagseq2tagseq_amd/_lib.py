@@ -1,0 +1,86 @@
+"""ctypes binding of libt2t_attn.so (declarations: include/t2t_attn.h).
+
+The library is the only compute path: if it is missing or cannot be loaded,
+every entry point raises.  There is no CPU fallback.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+from typing import List
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libt2t_attn.so")
+HEADER_PATH = os.path.join(os.path.dirname(HERE), "include", "t2t_attn.h")
+
+T2T_OK = 0
+T2T_DTYPE_BF16 = 0
+TILE = 128
+MAX_WORDS = 8
+
+
+class T2TTensor(ctypes.Structure):
+    _fields_ = [("data", ctypes.c_void_p), ("stride_b", ctypes.c_int64),
+                ("stride_h", ctypes.c_int64), ("stride_t", ctypes.c_int64)]
+
+
+class T2TMask(ctypes.Structure):
+    _fields_ = [("doc", ctypes.c_void_p), ("q_bits", ctypes.c_void_p),
+                ("kv_bits", ctypes.c_void_p), ("words", ctypes.c_int32),
+                ("mask_batch", ctypes.c_int32),
+                ("kv_num", ctypes.c_void_p), ("kv_idx", ctypes.c_void_p),
+                ("full_kv_num", ctypes.c_void_p), ("full_kv_idx", ctypes.c_void_p),
+                ("q_num", ctypes.c_void_p), ("q_idx", ctypes.c_void_p),
+                ("full_q_num", ctypes.c_void_p), ("full_q_idx", ctypes.c_void_p)]
+
+
+_lib = None
+
+_P = ctypes.c_void_p
+_I32 = ctypes.c_int32
+_SIGS = {
+    "t2t_version": ([], ctypes.c_char_p),
+    "t2t_last_error": ([], ctypes.c_char_p),
+    "t2t_mask_meta": ([_P, _P, _P, _I32, _I32, _I32] + [_P] * 9 + [_P], ctypes.c_int),
+    "t2t_attn_fwd": ([_P] * 5 + [_I32] * 6 + [ctypes.c_float, _P, _P], ctypes.c_int),
+    "t2t_attn_bwd": ([_P] * 10 + [_I32] * 6 + [ctypes.c_float, _P, _P], ctypes.c_int),
+}
+
+
+def header_functions() -> List[str]:
+    """Names of the functions include/t2t_attn.h declares."""
+    with open(HEADER_PATH) as f:
+        text = f.read()
+    return re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(t2t_\w+)\s*\(", text, flags=re.M)
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"{LIB_PATH} is not built; run `python -m tagseq2tagseq_amd.build` "
+                "(the masked-attention path has no CPU fallback)")
+        l = ctypes.CDLL(LIB_PATH)
+        for name, (args, res) in _SIGS.items():
+            fn = getattr(l, name)
+            fn.argtypes = args
+            fn.restype = res
+        _lib = l
+    return _lib
+
+
+def check(rc: int, what: str) -> None:
+    if rc != T2T_OK:
+        msg = lib().t2t_last_error().decode(errors="replace")
+        raise RuntimeError(f"{what} failed (status {rc}): {msg}")
+
+
+def tensor_struct(t) -> T2TTensor:
+    """[B, H, T, D] torch tensor with unit stride along D."""
+    if t.dim() != 4:
+        raise ValueError(f"expected a 4-D [B, H, T, D] tensor, got shape {tuple(t.shape)}")
+    if t.stride(3) != 1:
+        raise ValueError("the head dimension (last) must have unit stride")
+    return T2TTensor(t.data_ptr(), t.stride(0), t.stride(1), t.stride(2))

@@ -1,0 +1,214 @@
+"""Masked attention entry points: the ``flex_attention`` seam, its autograd
+Function and a ``FlexSelfAttention``-shaped module.
+
+Seams replaced (reference file:line):
+  * ``flex_attention(q, k, v, block_mask=..., scale=None, enable_gqa=False)`` --
+    the module-global symbol the reference's attention module calls
+    (model/modules/layer.py:16-21,33; monkey-patched at generate.py:167-178),
+    i.e. torch/nn/attention/flex_attention.py:1396-1676.
+  * ``T2TFlexAttentionFn`` -- in place of FlexAttentionAutogradOp
+    (torch/_higher_order_ops/flex_attention.py:628-767): saves q, k, v, out and
+    the log2-domain LSE; backward runs the atomic-free dK/dV + dQ kernels.
+  * ``FlexSelfAttention(dim, num_heads, max_seq_len, fp8_out_proj)`` with
+    ``forward(x, block_mask)`` -- the constructor / call signature the
+    reference's Layer uses (model/modules/layer.py:16-21,33).
+
+All compute runs in libt2t_attn.so on the current ROCm stream.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+from typing import Optional
+
+import torch
+import torch.nn as nn
+
+from . import _lib
+from .block_mask import T2TBlockMask
+
+LN2 = math.log(2.0)
+_DTYPE_CODES = {torch.bfloat16: _lib.T2T_DTYPE_BF16}
+
+
+def _stream_ptr(t: torch.Tensor) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def _view(t: torch.Tensor) -> _lib.T2TTensor:
+    s = _lib.tensor_struct(t)
+    # size-1 dims may carry arbitrary strides; they are never stepped
+    if t.shape[0] == 1:
+        s.stride_b = 0
+    if t.shape[1] == 1:
+        s.stride_h = 0
+    return s
+
+
+def _validate(q, k, v, block_mask, enable_gqa):
+    """Shape rules of torch/nn/attention/flex_attention.py:1473-1541."""
+    if not isinstance(block_mask, T2TBlockMask):
+        raise TypeError("block_mask must be a T2TBlockMask (build one with the mask creators "
+                        "in tagseq2tagseq_amd.mask_creators)")
+    if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
+        raise ValueError("query, key, value must be 4-D [B, H, T, D]")
+    if not (q.dtype == k.dtype == v.dtype):
+        raise ValueError(f"dtype mismatch: {q.dtype}, {k.dtype}, {v.dtype}")
+    if q.dtype not in _DTYPE_CODES:
+        raise NotImplementedError(f"dtype {q.dtype} is not supported (bfloat16 only)")
+    if not (q.is_cuda and k.is_cuda and v.is_cuda):
+        raise RuntimeError("the masked-attention kernels need ROCm GPU tensors")
+    B, Hq, T, D = q.shape
+    if k.shape[0] != B or v.shape[0] != B:
+        raise ValueError("batch sizes of query, key, value differ")
+    if k.shape[2] != T or v.shape[2] != T:
+        raise ValueError("query and key/value sequence lengths must match (self-attention)")
+    if k.shape[3] != D or v.shape[3] != D:
+        raise ValueError("query, key and value head dims must match")
+    if k.shape[1] != v.shape[1]:
+        raise ValueError("key and value head counts differ")
+    Hkv = k.shape[1]
+    if Hq != Hkv:
+        if not enable_gqa:
+            raise ValueError(f"Expect query and key/value to have the same number of heads but got "
+                             f"Hq={Hq} and Hkv={Hkv}. Try setting enable_gqa=True for GQA.")
+        if Hq % Hkv != 0:
+            raise ValueError(f"Expect number of query heads to be a multiple of kv heads for GQA "
+                             f"but got Hq={Hq} and Hkv={Hkv}.")
+    if block_mask.seq_len != T:
+        raise ValueError(f"block_mask was built for T={block_mask.seq_len} but inputs have T={T}")
+    if block_mask.mask_batch not in (1, B):
+        raise ValueError(f"block_mask batch {block_mask.mask_batch} does not broadcast to B={B}")
+    if D not in (64, 128):
+        raise NotImplementedError(f"head dim {D} is not supported (64 or 128)")
+    return B, Hq, Hkv, T, D
+
+
+def attn_fwd(q, k, v, block_mask: T2TBlockMask, scale: float):
+    """Kernel call: returns (out [B,Hq,T,D] in q.dtype, lse2 float32 [B,Hq,T])."""
+    B, Hq, Hkv, T, D = q.shape[0], q.shape[1], k.shape[1], q.shape[2], q.shape[3]
+    out = torch.empty((B, Hq, T, D), dtype=q.dtype, device=q.device)
+    lse2 = torch.empty((B, Hq, T), dtype=torch.float32, device=q.device)
+    qs, ks, vs, os_ = _view(q), _view(k), _view(v), _view(out)
+    with torch.cuda.device(q.device):
+        rc = _lib.lib().t2t_attn_fwd(ctypes.byref(qs), ctypes.byref(ks), ctypes.byref(vs),
+                                     ctypes.byref(os_), lse2.data_ptr(), B, Hq, Hkv, T, D,
+                                     _DTYPE_CODES[q.dtype], float(scale),
+                                     ctypes.byref(block_mask.c_struct()), _stream_ptr(q))
+    _lib.check(rc, "t2t_attn_fwd")
+    return out, lse2
+
+
+def attn_bwd(q, k, v, out, dout, lse2, block_mask: T2TBlockMask, scale: float):
+    """Kernel call: returns (dq, dk, dv)."""
+    B, Hq, Hkv, T, D = q.shape[0], q.shape[1], k.shape[1], q.shape[2], q.shape[3]
+    if dout.stride(3) != 1:
+        dout = dout.contiguous()
+    dq = torch.empty_like(q, memory_format=torch.contiguous_format)
+    dk = torch.empty_like(k, memory_format=torch.contiguous_format)
+    dv = torch.empty_like(v, memory_format=torch.contiguous_format)
+    delta = torch.empty((B, Hq, T), dtype=torch.float32, device=q.device)
+    views = [_view(t) for t in (q, k, v, out, dout)]
+    gviews = [_view(t) for t in (dq, dk, dv)]
+    with torch.cuda.device(q.device):
+        rc = _lib.lib().t2t_attn_bwd(*[ctypes.byref(x) for x in views], lse2.data_ptr(),
+                                     delta.data_ptr(), *[ctypes.byref(x) for x in gviews],
+                                     B, Hq, Hkv, T, D, _DTYPE_CODES[q.dtype], float(scale),
+                                     ctypes.byref(block_mask.c_struct()), _stream_ptr(q))
+    _lib.check(rc, "t2t_attn_bwd")
+    return dq, dk, dv
+
+
+class T2TFlexAttentionFn(torch.autograd.Function):
+    """autograd.Function over the gfx950 kernels (in place of
+    FlexAttentionAutogradOp, torch/_higher_order_ops/flex_attention.py:628-767)."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, block_mask, scale):
+        out, lse2 = attn_fwd(q, k, v, block_mask, scale)
+        ctx.save_for_backward(q, k, v, out, lse2)
+        ctx.block_mask = block_mask
+        ctx.scale = scale
+        ctx.mark_non_differentiable(lse2)
+        return out, lse2
+
+    @staticmethod
+    def backward(ctx, dout, _dlse2):
+        q, k, v, out, lse2 = ctx.saved_tensors
+        dq, dk, dv = attn_bwd(q, k, v, out, dout, lse2, ctx.block_mask, ctx.scale)
+        return dq, dk, dv, None, None
+
+
+def flex_attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
+                   score_mod=None, block_mask: Optional[T2TBlockMask] = None,
+                   scale: Optional[float] = None, enable_gqa: bool = False,
+                   return_lse: bool = False, kernel_options=None):
+    """Drop-in for torch's flex_attention on the doc_causal / cross_doc_link
+    path (torch/nn/attention/flex_attention.py:1396-1676).
+
+    ``score_mod`` must be None (the reference passes none).  The returned LSE is
+    in natural log, as torch's (internal log2 value times ln 2, :1575-1600).
+    """
+    if score_mod is not None:
+        raise NotImplementedError("score_mod is not supported by the gfx950 masked-attention path")
+    if block_mask is None:
+        raise ValueError("block_mask is required (build it with tagseq2tagseq_amd.mask_creators)")
+    _, _, _, _, D = _validate(query, key, value, block_mask, enable_gqa)
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)  # torch/nn/attention/flex_attention.py:1544
+    out, lse2 = T2TFlexAttentionFn.apply(query, key, value, block_mask, float(scale))
+    if return_lse:
+        return out, lse2 * LN2
+    return out
+
+
+class Rotary(nn.Module):
+    """Rotary position embedding on [B, H, T, D] (half-split pairs, base 10000)."""
+
+    def __init__(self, head_dim: int, max_seq_len: int, base: float = 10000.0):
+        super().__init__()
+        inv = base ** (-torch.arange(0, head_dim // 2, dtype=torch.float32) / (head_dim // 2))
+        t = torch.arange(max_seq_len, dtype=torch.float32)
+        freqs = torch.outer(t, inv)
+        self.register_buffer("cos", freqs.cos(), persistent=False)
+        self.register_buffer("sin", freqs.sin(), persistent=False)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        T = x.shape[-2]
+        cos = self.cos[:T].to(x.dtype)
+        sin = self.sin[:T].to(x.dtype)
+        x1, x2 = x.chunk(2, dim=-1)
+        return torch.cat((x1 * cos + x2 * sin, x2 * cos - x1 * sin), dim=-1)
+
+
+class FlexSelfAttention(nn.Module):
+    """Self-attention with the constructor and call signature the reference's
+    Layer uses (model/modules/layer.py:16-21, 33): QKV projection, rotary
+    embedding, masked attention on the gfx950 kernels, output projection.
+
+    The reference's module comes from the absent ``tunalab`` package; its
+    internal details (RoPE variant, QK-norm, fp8 out-projection) are not
+    available here, so ``fp8_out_proj`` is accepted and ignored.
+    """
+
+    def __init__(self, dim: int, num_heads: int, max_seq_len: int, fp8_out_proj: bool = False):
+        super().__init__()
+        if dim % num_heads != 0:
+            raise ValueError("dim must be divisible by num_heads")
+        self.dim = dim
+        self.num_heads = num_heads
+        self.head_dim = dim // num_heads
+        self.qkv = nn.Linear(dim, 3 * dim, bias=False)
+        self.proj = nn.Linear(dim, dim, bias=False)
+        self.rotary = Rotary(self.head_dim, max_seq_len)
+        self.fp8_out_proj = fp8_out_proj
+
+    def forward(self, x: torch.Tensor, block_mask: T2TBlockMask) -> torch.Tensor:
+        B, T, C = x.shape
+        qkv = self.qkv(x).view(B, T, 3, self.num_heads, self.head_dim)
+        q, k, v = qkv.unbind(dim=2)
+        q = self.rotary(q.transpose(1, 2))
+        k = self.rotary(k.transpose(1, 2))
+        v = v.transpose(1, 2)
+        y = flex_attention(q, k, v, block_mask=block_mask)
+        return self.proj(y.transpose(1, 2).reshape(B, T, C))

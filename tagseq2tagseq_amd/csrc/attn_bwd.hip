@@ -1,0 +1,409 @@
+// Masked flash-attention backward, bf16 in / fp32 accumulate, gfx950 MFMA.
+//
+// Arithmetic of torch's sdpa_dense_backward
+// (torch/_higher_order_ops/flex_attention.py:825-994):
+//   P  = exp(S - LSE) on allowed pairs (0 elsewhere)
+//   dV = P^T dO                       Delta = rowsum(O * dO)
+//   dP = dO V^T                       dS = P * (dP - Delta)
+//   dQ = dS K * scale                 dK = dS^T Q * scale
+// with dK / dV summed over the query heads that share a KV head (GQA).
+//
+// Three launches, none of them atomic:
+//   1. bwd_delta:  Delta per query row.
+//   2. bwd_dkdv:   one work-group per (b, kv head, 128-key tile); walks the
+//                  column's partial and full query tiles (q_num_blocks /
+//                  q_indices, full_q_*) for every query head of the group and
+//                  accumulates dK, dV in registers -- deterministic.
+//   3. bwd_dq:     one work-group per (b, query head, 128-query tile); walks
+//                  the row's KV tiles and accumulates dQ in registers.
+#include "attn_kernels.h"
+
+namespace t2t {
+
+namespace {
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+struct BwdParams {
+  const __bf16* q; int64_t q_sb, q_sh, q_st;
+  const __bf16* k; int64_t k_sb, k_sh, k_st;
+  const __bf16* v; int64_t v_sb, v_sh, v_st;
+  const __bf16* o; int64_t o_sb, o_sh, o_st;
+  const __bf16* dout; int64_t do_sb, do_sh, do_st;
+  __bf16* dq; int64_t dq_sb, dq_sh, dq_st;
+  __bf16* dk; int64_t dk_sb, dk_sh, dk_st;
+  __bf16* dv; int64_t dv_sb, dv_sh, dv_st;
+  const float* lse2;  // [B][Hq][T], log2 domain of scaled scores
+  float* delta;       // [B][Hq][T]
+  int B, Hq, Hkv, T, nt;
+  float scale, scale_log2;
+  MaskTables m;
+};
+
+template <int D, int PITCH>
+__device__ __forceinline__ void load_tile(__bf16* dst, const __bf16* src, int64_t st, int t0,
+                                          int T, int tid) {
+  constexpr int kChunks = D / 8;
+  constexpr int kIters = kTile * kChunks / kThreads;
+  uint4 buf[kIters];
+#pragma unroll
+  for (int it = 0; it < kIters; ++it) {
+    const int c = tid + it * kThreads;
+    const int r = c / kChunks, col = (c % kChunks) * 8;
+    const int t = t0 + r;
+    buf[it] = (t < T) ? *reinterpret_cast<const uint4*>(src + (int64_t)t * st + col)
+                      : make_uint4(0, 0, 0, 0);
+  }
+#pragma unroll
+  for (int it = 0; it < kIters; ++it) {
+    const int c = tid + it * kThreads;
+    const int r = c / kChunks, col = (c % kChunks) * 8;
+    *reinterpret_cast<uint4*>(dst + r * PITCH + col) = buf[it];
+  }
+}
+
+// Stores a transposed 32 x 32 f32 accumulator block (rows = d, cols = token)
+// scaled by `mul` as bf16 into out[token][d0 + d].
+__device__ __forceinline__ void store_acc_t(__bf16* out_row, const f32x16& acc, int d0, int g,
+                                            float mul) {
+#pragma unroll
+  for (int i = 0; i < 16; i += 4) {
+    bf16x4 w4;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) w4[e] = (__bf16)(acc[i + e] * mul);
+    *reinterpret_cast<bf16x4*>(out_row + d0 + acc_row(i, g)) = w4;
+  }
+}
+
+}  // namespace
+
+// Delta[b, h, t] = sum_d O * dO.  16 lanes per row, 8 d-values per lane.
+template <int D>
+__global__ __launch_bounds__(kThreads) void bwd_delta_kernel(BwdParams p) {
+  constexpr int kLanesPerRow = D / 8;
+  constexpr int kRowsPerBlock = kThreads / kLanesPerRow;
+  const int tid = threadIdx.x;
+  const int sub = tid % kLanesPerRow;
+  const int64_t rowid = (int64_t)blockIdx.x * kRowsPerBlock + tid / kLanesPerRow;
+  const int64_t nrows = (int64_t)p.B * p.Hq * p.T;
+  float acc = 0.f;
+  if (rowid < nrows) {
+    const int t = (int)(rowid % p.T);
+    const int h = (int)((rowid / p.T) % p.Hq);
+    const int b = (int)(rowid / ((int64_t)p.T * p.Hq));
+    const bf16x8 ov = *reinterpret_cast<const bf16x8*>(p.o + b * p.o_sb + h * p.o_sh + (int64_t)t * p.o_st + 8 * sub);
+    const bf16x8 gv = *reinterpret_cast<const bf16x8*>(p.dout + b * p.do_sb + h * p.do_sh + (int64_t)t * p.do_st + 8 * sub);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc += (float)ov[j] * (float)gv[j];
+  }
+#pragma unroll
+  for (int off = kLanesPerRow / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
+  if (rowid < nrows && sub == 0) p.delta[rowid] = acc;
+}
+
+template <int D>
+struct DkdvSmem {
+  static constexpr int kPitch = D + 8;
+  __bf16 q[kTile * kPitch];
+  __bf16 dout[kTile * kPitch];
+  float lse2[kTile];
+  float delta[kTile];
+  int32_t qdoc[kTile];
+  uint64_t qbits[kMaxWords][kTile];
+};
+
+template <int D>
+__global__ __launch_bounds__(kThreads, 1) void bwd_dkdv_kernel(BwdParams p) {
+  constexpr int PITCH = DkdvSmem<D>::kPitch;
+  constexpr int KS = D / 16;
+  constexpr int DT = D / 32;
+  __shared__ DkdvSmem<D> sm;
+
+  const int kt = blockIdx.x, hk = blockIdx.y, b = blockIdx.z;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int g = lane >> 5, n = lane & 31;
+  const int G = p.Hq / p.Hkv;
+  const int mb = p.m.Bm > 1 ? b : 0;
+  const int T = p.T, nt = p.nt, words = p.m.words;
+  const int k0 = kt * kTile;
+  const int key = k0 + 32 * wave + n;
+  const bool kvalid = key < T;
+
+  // K and V as the B operand (k = d, n = key): lane (g, n) holds row `key`.
+  bf16x8 kf[KS], vf[KS];
+  {
+    const int kr = kvalid ? key : 0;
+    const __bf16* kp = p.k + b * p.k_sb + hk * p.k_sh + (int64_t)kr * p.k_st;
+    const __bf16* vp = p.v + b * p.v_sb + hk * p.v_sh + (int64_t)kr * p.v_st;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      const bf16x8 a = *reinterpret_cast<const bf16x8*>(kp + 16 * s + 8 * g);
+      const bf16x8 c = *reinterpret_cast<const bf16x8*>(vp + 16 * s + 8 * g);
+      kf[s] = kvalid ? a : bf16x8{};
+      vf[s] = kvalid ? c : bf16x8{};
+    }
+  }
+  const int32_t* mdoc = p.m.doc + (size_t)mb * T;
+  const uint64_t* mqb = p.m.qbits + (size_t)mb * words * T;
+  const uint64_t* mkb = p.m.kvbits + (size_t)mb * words * T;
+  const int32_t kdoc = kvalid ? mdoc[key] : 0;
+  uint64_t kbits[kMaxWords];
+#pragma unroll
+  for (int w = 0; w < kMaxWords; ++w) kbits[w] = (w < words && kvalid) ? mkb[(size_t)w * T + key] : 0ull;
+
+  const size_t col = (size_t)mb * nt + kt;
+  const int npart = p.m.q_num[col];
+  const int nfull = p.m.full_q_num[col];
+  const int32_t* pidx = p.m.q_idx + col * nt;
+  const int32_t* fidx = p.m.full_q_idx + col * nt;
+
+  f32x16 dkacc[DT], dvacc[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) { dkacc[dt] = f32x16{}; dvacc[dt] = f32x16{}; }
+
+  for (int hh = 0; hh < G; ++hh) {
+    const int h = hk * G + hh;
+    const __bf16* qbase = p.q + b * p.q_sb + h * p.q_sh;
+    const __bf16* dobase = p.dout + b * p.do_sb + h * p.do_sh;
+    const float* lrow = p.lse2 + ((size_t)b * p.Hq + h) * T;
+    const float* drow = p.delta + ((size_t)b * p.Hq + h) * T;
+    for (int it = 0; it < npart + nfull; ++it) {
+      const bool partial = it < npart;
+      const int qt = partial ? pidx[it] : fidx[it - npart];
+      const int q0 = qt * kTile;
+      __syncthreads();
+      load_tile<D, PITCH>(sm.q, qbase, p.q_st, q0, T, tid);
+      load_tile<D, PITCH>(sm.dout, dobase, p.do_st, q0, T, tid);
+      if (tid < kTile) {
+        const int t = q0 + tid;
+        const float l = t < T ? lrow[t] : -INFINITY;
+        // Fully masked rows (LSE = -inf) carry P = 0: park them at +inf so
+        // exp2(s - lse) vanishes.
+        sm.lse2[tid] = (l == -INFINITY) ? INFINITY : l;
+        sm.delta[tid] = t < T ? drow[t] : 0.f;
+        if (partial) {
+          sm.qdoc[tid] = t < T ? mdoc[t] : 0;
+          for (int w = 0; w < words; ++w) sm.qbits[w][tid] = t < T ? mqb[(size_t)w * T + t] : 0ull;
+        }
+      }
+      __syncthreads();
+
+#pragma unroll 1
+      for (int qs = 0; qs < 4; ++qs) {
+        // S and dP for 32 queries x this wave's 32 keys.
+        f32x16 sacc = f32x16{}, dpacc = f32x16{};
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+          const bf16x8 qa = lds_row8(&sm.q[(32 * qs + n) * PITCH + 16 * s + 8 * g]);
+          const bf16x8 da = lds_row8(&sm.dout[(32 * qs + n) * PITCH + 16 * s + 8 * g]);
+          sacc = mfma32(qa, kf[s], sacc);
+          dpacc = mfma32(da, vf[s], dpacc);
+        }
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int qq = 32 * qs + acc_row(i, g);
+          const int qrow = q0 + qq;
+          float pv = fast_exp2(sacc[i] * p.scale_log2 - sm.lse2[qq]);
+          if (partial) {
+            bool ok = kvalid && qrow < T && key <= qrow;
+            if (ok && sm.qdoc[qq] != kdoc) {
+              bool hit = false;
+              for (int w = 0; w < words; ++w) hit |= (sm.qbits[w][qq] & kbits[w]) != 0ull;
+              ok = hit;
+            }
+            if (!ok) pv = 0.f;
+          }
+          sacc[i] = pv;                                  // P
+          dpacc[i] = pv * (dpacc[i] - sm.delta[qq]);     // dS
+        }
+        // dV^T += dO^T P, dK^T += Q^T dS (contraction over the 32 queries).
+#pragma unroll
+        for (int h2 = 0; h2 < 2; ++h2) {
+          const bf16x8 pb = pack_half(sacc, h2);
+          const bf16x8 sb = pack_half(dpacc, h2);
+#pragma unroll
+          for (int dt = 0; dt < DT; ++dt) {
+            const bf16x8 doa = lds_col8(sm.dout, PITCH, 32 * qs + 16 * h2, 8, 32 * dt, lane);
+            const bf16x8 qa = lds_col8(sm.q, PITCH, 32 * qs + 16 * h2, 8, 32 * dt, lane);
+            dvacc[dt] = mfma32(doa, pb, dvacc[dt]);
+            dkacc[dt] = mfma32(qa, sb, dkacc[dt]);
+          }
+        }
+      }
+    }
+  }
+
+  if (kvalid) {
+    __bf16* dkp = p.dk + b * p.dk_sb + hk * p.dk_sh + (int64_t)key * p.dk_st;
+    __bf16* dvp = p.dv + b * p.dv_sb + hk * p.dv_sh + (int64_t)key * p.dv_st;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      store_acc_t(dkp, dkacc[dt], 32 * dt, g, p.scale);
+      store_acc_t(dvp, dvacc[dt], 32 * dt, g, 1.f);
+    }
+  }
+}
+
+template <int D>
+struct DqSmem {
+  static constexpr int kPitch = D + 8;
+  __bf16 k[kTile * kPitch];
+  __bf16 v[kTile * kPitch];
+  int32_t kdoc[kTile];
+  uint64_t kbits[kMaxWords][kTile];
+};
+
+template <int D>
+__global__ __launch_bounds__(kThreads, 1) void bwd_dq_kernel(BwdParams p) {
+  constexpr int PITCH = DqSmem<D>::kPitch;
+  constexpr int KS = D / 16;
+  constexpr int DT = D / 32;
+  __shared__ DqSmem<D> sm;
+
+  const int qt = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int g = lane >> 5, n = lane & 31;
+  const int hk = h / (p.Hq / p.Hkv);
+  const int mb = p.m.Bm > 1 ? b : 0;
+  const int T = p.T, nt = p.nt, words = p.m.words;
+  const int q0 = qt * kTile;
+  const int qrow = q0 + 32 * wave + n;
+  const bool qvalid = qrow < T;
+
+  bf16x8 qf[KS], dof[KS];
+  {
+    const int qr = qvalid ? qrow : 0;
+    const __bf16* qp = p.q + b * p.q_sb + h * p.q_sh + (int64_t)qr * p.q_st;
+    const __bf16* dp = p.dout + b * p.do_sb + h * p.do_sh + (int64_t)qr * p.do_st;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      const bf16x8 a = *reinterpret_cast<const bf16x8*>(qp + 16 * s + 8 * g);
+      const bf16x8 c = *reinterpret_cast<const bf16x8*>(dp + 16 * s + 8 * g);
+      qf[s] = qvalid ? a : bf16x8{};
+      dof[s] = qvalid ? c : bf16x8{};
+    }
+  }
+  float lse2 = INFINITY, delta = 0.f;
+  if (qvalid) {
+    const float l = p.lse2[((size_t)b * p.Hq + h) * T + qrow];
+    lse2 = (l == -INFINITY) ? INFINITY : l;
+    delta = p.delta[((size_t)b * p.Hq + h) * T + qrow];
+  }
+  const int32_t* mdoc = p.m.doc + (size_t)mb * T;
+  const uint64_t* mqb = p.m.qbits + (size_t)mb * words * T;
+  const uint64_t* mkb = p.m.kvbits + (size_t)mb * words * T;
+  const int32_t qdoc = qvalid ? mdoc[qrow] : 0;
+  uint64_t qbits[kMaxWords];
+#pragma unroll
+  for (int w = 0; w < kMaxWords; ++w) qbits[w] = (w < words && qvalid) ? mqb[(size_t)w * T + qrow] : 0ull;
+
+  const __bf16* kbase = p.k + b * p.k_sb + hk * p.k_sh;
+  const __bf16* vbase = p.v + b * p.v_sb + hk * p.v_sh;
+  const size_t row = (size_t)mb * nt + qt;
+  const int npart = p.m.kv_num[row];
+  const int nfull = p.m.full_kv_num[row];
+  const int32_t* pidx = p.m.kv_idx + row * nt;
+  const int32_t* fidx = p.m.full_kv_idx + row * nt;
+
+  f32x16 dqacc[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) dqacc[dt] = f32x16{};
+
+  for (int it = 0; it < npart + nfull; ++it) {
+    const bool partial = it < npart;
+    const int kt = partial ? pidx[it] : fidx[it - npart];
+    const int k0 = kt * kTile;
+    __syncthreads();
+    load_tile<D, PITCH>(sm.k, kbase, p.k_st, k0, T, tid);
+    load_tile<D, PITCH>(sm.v, vbase, p.v_st, k0, T, tid);
+    if (partial && tid < kTile) {
+      const int t = k0 + tid;
+      sm.kdoc[tid] = t < T ? mdoc[t] : 0;
+      for (int w = 0; w < words; ++w) sm.kbits[w][tid] = t < T ? mkb[(size_t)w * T + t] : 0ull;
+    }
+    __syncthreads();
+
+#pragma unroll 1
+    for (int j = 0; j < 4; ++j) {
+      f32x16 sacc = f32x16{}, dpacc = f32x16{};
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        const bf16x8 ka = lds_row8(&sm.k[(32 * j + n) * PITCH + 16 * s + 8 * g]);
+        const bf16x8 va = lds_row8(&sm.v[(32 * j + n) * PITCH + 16 * s + 8 * g]);
+        sacc = mfma32(ka, qf[s], sacc);
+        dpacc = mfma32(va, dof[s], dpacc);
+      }
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int kk = 32 * j + acc_row(i, g);
+        const int keyi = k0 + kk;
+        float pv = fast_exp2(sacc[i] * p.scale_log2 - lse2);
+        if (partial) {
+          bool ok = qvalid && keyi < T && keyi <= qrow;
+          if (ok && qdoc != sm.kdoc[kk]) {
+            bool hit = false;
+            for (int w = 0; w < words; ++w) hit |= (qbits[w] & sm.kbits[w][kk]) != 0ull;
+            ok = hit;
+          }
+          if (!ok) pv = 0.f;
+        }
+        dpacc[i] = pv * (dpacc[i] - delta);  // dS^T
+      }
+      // dQ^T += K^T dS^T (contraction over the 32 keys of block j).
+#pragma unroll
+      for (int h2 = 0; h2 < 2; ++h2) {
+        const bf16x8 sb = pack_half(dpacc, h2);
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+          const bf16x8 ka = lds_col8(sm.k, PITCH, 32 * j + 16 * h2, 8, 32 * dt, lane);
+          dqacc[dt] = mfma32(ka, sb, dqacc[dt]);
+        }
+      }
+    }
+  }
+
+  if (qvalid) {
+    __bf16* dqp = p.dq + b * p.dq_sb + h * p.dq_sh + (int64_t)qrow * p.dq_st;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) store_acc_t(dqp, dqacc[dt], 32 * dt, g, p.scale);
+  }
+}
+
+hipError_t launch_attn_bwd_bf16(const TensorView& q, const TensorView& k, const TensorView& v,
+                                const TensorView& o, const TensorView& dout, const float* lse2,
+                                float* delta, const TensorView& dq, const TensorView& dk,
+                                const TensorView& dv, const AttnDims& dims,
+                                const MaskTables& mask, hipStream_t stream) {
+  BwdParams p;
+  p.q = static_cast<const __bf16*>(q.data); p.q_sb = q.sb; p.q_sh = q.sh; p.q_st = q.st;
+  p.k = static_cast<const __bf16*>(k.data); p.k_sb = k.sb; p.k_sh = k.sh; p.k_st = k.st;
+  p.v = static_cast<const __bf16*>(v.data); p.v_sb = v.sb; p.v_sh = v.sh; p.v_st = v.st;
+  p.o = static_cast<const __bf16*>(o.data); p.o_sb = o.sb; p.o_sh = o.sh; p.o_st = o.st;
+  p.dout = static_cast<const __bf16*>(dout.data); p.do_sb = dout.sb; p.do_sh = dout.sh; p.do_st = dout.st;
+  p.dq = static_cast<__bf16*>(dq.data); p.dq_sb = dq.sb; p.dq_sh = dq.sh; p.dq_st = dq.st;
+  p.dk = static_cast<__bf16*>(dk.data); p.dk_sb = dk.sb; p.dk_sh = dk.sh; p.dk_st = dk.st;
+  p.dv = static_cast<__bf16*>(dv.data); p.dv_sb = dv.sb; p.dv_sh = dv.sh; p.dv_st = dv.st;
+  p.lse2 = lse2;
+  p.delta = delta;
+  p.B = dims.B; p.Hq = dims.Hq; p.Hkv = dims.Hkv; p.T = dims.T;
+  p.nt = (dims.T + kTile - 1) / kTile;
+  p.scale = dims.scale;
+  p.scale_log2 = dims.scale * kLog2e;
+  p.m = mask;
+  if (p.nt == 0 || dims.B == 0 || dims.Hq == 0) return hipSuccess;
+  const int64_t rows = (int64_t)dims.B * dims.Hq * dims.T;
+  const int rows_per_block = kThreads / (dims.D / 8);
+  const dim3 dgrid((unsigned)((rows + rows_per_block - 1) / rows_per_block));
+  if (dims.D == 64) {
+    hipLaunchKernelGGL(bwd_delta_kernel<64>, dgrid, dim3(kThreads), 0, stream, p);
+    hipLaunchKernelGGL(bwd_dkdv_kernel<64>, dim3(p.nt, dims.Hkv, dims.B), dim3(kThreads), 0, stream, p);
+    hipLaunchKernelGGL(bwd_dq_kernel<64>, dim3(p.nt, dims.Hq, dims.B), dim3(kThreads), 0, stream, p);
+  } else {
+    hipLaunchKernelGGL(bwd_delta_kernel<128>, dgrid, dim3(kThreads), 0, stream, p);
+    hipLaunchKernelGGL(bwd_dkdv_kernel<128>, dim3(p.nt, dims.Hkv, dims.B), dim3(kThreads), 0, stream, p);
+    hipLaunchKernelGGL(bwd_dq_kernel<128>, dim3(p.nt, dims.Hq, dims.B), dim3(kThreads), 0, stream, p);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace t2t

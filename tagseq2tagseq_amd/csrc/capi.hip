@@ -1,0 +1,143 @@
+// extern "C" boundary of libt2t_attn.so: argument validation, error
+// reporting and dispatch to the gfx950 kernels.  No allocation happens here.
+#include <cstdarg>
+#include <cstdio>
+
+#include "../../include/t2t_attn.h"
+#include "attn_kernels.h"
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int hip_status(hipError_t e, const char* what) {
+  if (e == hipSuccess) return T2T_OK;
+  return fail(T2T_EHIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+bool view_ok(const t2t_tensor* t) {
+  return t && t->data && t->stride_b >= 0 && t->stride_h >= 0 && t->stride_t > 0 &&
+         (reinterpret_cast<uintptr_t>(t->data) % 16) == 0 && (t->stride_t % 8) == 0 &&
+         (t->stride_h % 8) == 0 && (t->stride_b % 8) == 0;
+}
+
+t2t::TensorView as_view(const t2t_tensor* t) {
+  return t2t::TensorView{t->data, t->stride_b, t->stride_h, t->stride_t};
+}
+
+int check_mask(const t2t_mask* m, int B, bool need_rows, bool need_cols) {
+  if (!m) return fail(T2T_EINVAL, "mask is NULL");
+  if (!m->doc) return fail(T2T_EINVAL, "mask.doc is NULL");
+  if (m->words < 0 || m->words > T2T_MAX_WORDS)
+    return fail(T2T_EUNSUPPORTED, "mask.words=%d outside [0, %d]", m->words, T2T_MAX_WORDS);
+  if (m->words > 0 && (!m->q_bits || !m->kv_bits))
+    return fail(T2T_EINVAL, "mask.words=%d but q_bits/kv_bits is NULL", m->words);
+  if (!(m->mask_batch == 1 || m->mask_batch == B))
+    return fail(T2T_EINVAL, "mask.mask_batch=%d must be 1 or B=%d", m->mask_batch, B);
+  if (need_rows && (!m->kv_num || !m->kv_idx || !m->full_kv_num || !m->full_kv_idx))
+    return fail(T2T_EINVAL, "mask row tables (kv_num/kv_idx/full_kv_*) missing");
+  if (need_cols && (!m->q_num || !m->q_idx || !m->full_q_num || !m->full_q_idx))
+    return fail(T2T_EINVAL, "mask column tables (q_num/q_idx/full_q_*) missing");
+  return T2T_OK;
+}
+
+t2t::MaskTables as_tables(const t2t_mask* m) {
+  t2t::MaskTables t;
+  t.doc = m->doc;
+  t.qbits = m->q_bits;
+  t.kvbits = m->kv_bits;
+  t.words = m->words;
+  t.Bm = m->mask_batch;
+  t.kv_num = m->kv_num; t.kv_idx = m->kv_idx;
+  t.full_kv_num = m->full_kv_num; t.full_kv_idx = m->full_kv_idx;
+  t.q_num = m->q_num; t.q_idx = m->q_idx;
+  t.full_q_num = m->full_q_num; t.full_q_idx = m->full_q_idx;
+  return t;
+}
+
+int check_dims(int B, int Hq, int Hkv, int T, int D, int dtype) {
+  if (B < 0 || Hq < 0 || Hkv <= 0 || T < 0) return fail(T2T_EINVAL, "negative size");
+  if (Hq % Hkv != 0)
+    return fail(T2T_EINVAL, "Hq=%d must be a multiple of Hkv=%d (GQA)", Hq, Hkv);
+  if (dtype != T2T_DTYPE_BF16) return fail(T2T_EUNSUPPORTED, "dtype %d not supported", dtype);
+  if (D != 64 && D != 128) return fail(T2T_EUNSUPPORTED, "head dim D=%d not in {64, 128}", D);
+  return T2T_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* t2t_version(void) { return "t2t_attn 0.1 gfx950"; }
+
+const char* t2t_last_error(void) { return g_err; }
+
+int t2t_mask_meta(const int32_t* doc, const uint64_t* q_bits, const uint64_t* kv_bits,
+                  int32_t mask_batch, int32_t T, int32_t words, int8_t* tile_class,
+                  int32_t* kv_num, int32_t* kv_idx, int32_t* full_kv_num,
+                  int32_t* full_kv_idx, int32_t* q_num, int32_t* q_idx,
+                  int32_t* full_q_num, int32_t* full_q_idx, void* stream) {
+  if (T < 0 || mask_batch < 0) return fail(T2T_EINVAL, "negative T or mask_batch");
+  if (words < 0 || words > T2T_MAX_WORDS)
+    return fail(T2T_EUNSUPPORTED, "words=%d outside [0, %d]", words, T2T_MAX_WORDS);
+  if (T == 0 || mask_batch == 0) return T2T_OK;
+  if (!doc || (words > 0 && (!q_bits || !kv_bits)) || !tile_class || !kv_num || !kv_idx ||
+      !full_kv_num || !full_kv_idx || !q_num || !q_idx || !full_q_num || !full_q_idx)
+    return fail(T2T_EINVAL, "NULL pointer argument");
+  return hip_status(t2t::launch_mask_meta(doc, q_bits, kv_bits, mask_batch, T, words,
+                                          tile_class, kv_num, kv_idx, full_kv_num, full_kv_idx,
+                                          q_num, q_idx, full_q_num, full_q_idx,
+                                          static_cast<hipStream_t>(stream)),
+                    "t2t_mask_meta launch");
+}
+
+int t2t_attn_fwd(const t2t_tensor* q, const t2t_tensor* k, const t2t_tensor* v,
+                 const t2t_tensor* o, float* lse2, int32_t B, int32_t Hq, int32_t Hkv,
+                 int32_t T, int32_t D, int32_t dtype, float scale, const t2t_mask* mask,
+                 void* stream) {
+  int rc = check_dims(B, Hq, Hkv, T, D, dtype);
+  if (rc) return rc;
+  if (B == 0 || Hq == 0 || T == 0) return T2T_OK;
+  if (!view_ok(q) || !view_ok(k) || !view_ok(v) || !view_ok(o))
+    return fail(T2T_EINVAL, "q/k/v/o view invalid (NULL, misaligned or bad stride)");
+  if (!lse2) return fail(T2T_EINVAL, "lse2 is NULL");
+  rc = check_mask(mask, B, true, false);
+  if (rc) return rc;
+  t2t::AttnDims dims{B, Hq, Hkv, T, D, scale};
+  return hip_status(t2t::launch_attn_fwd_bf16(as_view(q), as_view(k), as_view(v), as_view(o),
+                                              lse2, dims, as_tables(mask),
+                                              static_cast<hipStream_t>(stream)),
+                    "t2t_attn_fwd launch");
+}
+
+int t2t_attn_bwd(const t2t_tensor* q, const t2t_tensor* k, const t2t_tensor* v,
+                 const t2t_tensor* o, const t2t_tensor* dout, const float* lse2,
+                 float* delta, const t2t_tensor* dq, const t2t_tensor* dk,
+                 const t2t_tensor* dv, int32_t B, int32_t Hq, int32_t Hkv, int32_t T,
+                 int32_t D, int32_t dtype, float scale, const t2t_mask* mask, void* stream) {
+  int rc = check_dims(B, Hq, Hkv, T, D, dtype);
+  if (rc) return rc;
+  if (B == 0 || Hq == 0 || T == 0) return T2T_OK;
+  if (!view_ok(q) || !view_ok(k) || !view_ok(v) || !view_ok(o) || !view_ok(dout) ||
+      !view_ok(dq) || !view_ok(dk) || !view_ok(dv))
+    return fail(T2T_EINVAL, "tensor view invalid (NULL, misaligned or bad stride)");
+  if (!lse2 || !delta) return fail(T2T_EINVAL, "lse2/delta is NULL");
+  rc = check_mask(mask, B, true, true);
+  if (rc) return rc;
+  t2t::AttnDims dims{B, Hq, Hkv, T, D, scale};
+  return hip_status(
+      t2t::launch_attn_bwd_bf16(as_view(q), as_view(k), as_view(v), as_view(o), as_view(dout),
+                                lse2, delta, as_view(dq), as_view(dk), as_view(dv), dims,
+                                as_tables(mask), static_cast<hipStream_t>(stream)),
+      "t2t_attn_bwd launch");
+}
+
+}  // extern "C"

@@ -1,0 +1,130 @@
+"""GPU parity of the masked-attention forward / backward kernels.
+
+Small cases: against the float64 CPU oracle (oracle/attn_oracle.py).
+Full-size configs: against a chunked fp32 torch reference on the GPU over a
+subset of heads.  bf16 tolerance 2e-2 (abs and rel), the north-star bound.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attn_oracle as ao
+from oracle import mask_oracle as mo
+from tagseq2tagseq_amd import synth
+from tagseq2tagseq_amd.attention import flex_attention
+from tagseq2tagseq_amd.block_mask import build_block_mask
+from tests.helpers import (assert_close, random_row, row_arrays, to_dev_words,
+                           torch_ref_attention)
+
+pytestmark = pytest.mark.gpu
+
+ATOL = RTOL = 2e-2
+
+
+def _mask_from_rows(rows_np, device):
+    doc = torch.stack([torch.from_numpy(r[0]) for r in rows_np]).to(device)
+    if rows_np[0][1] is None:
+        return build_block_mask(doc)
+    qb = torch.stack([to_dev_words(r[1], device) for r in rows_np])
+    kb = torch.stack([to_dev_words(r[2], device) for r in rows_np])
+    return build_block_mask(doc, qb, kb)
+
+
+def _inputs(B, Hq, Hkv, T, D, seed, device, dtype=torch.bfloat16):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(B, Hq, T, D, generator=g).to(dtype)
+    k = torch.randn(B, Hkv, T, D, generator=g).to(dtype)
+    v = torch.randn(B, Hkv, T, D, generator=g).to(dtype)
+    do = torch.randn(B, Hq, T, D, generator=g).to(dtype)
+    return [t.to(device) for t in (q, k, v, do)]
+
+
+def _oracle_check(rows_np, B, Hq, Hkv, T, D, seed, device, bwd=True):
+    bm = _mask_from_rows(rows_np, device)
+    q, k, v, do = _inputs(B, Hq, Hkv, T, D, seed, device)
+    q.requires_grad_(True); k.requires_grad_(True); v.requires_grad_(True)
+    out, lse = flex_attention(q, k, v, block_mask=bm, enable_gqa=Hq != Hkv, return_lse=True)
+    dense = np.stack([mo.dense_mask(*r) for r in rows_np])
+    qn, kn, vn, don = (t.detach().float().cpu().numpy() for t in (q, k, v, do))
+    o_ref, lse_ref = ao.attention_fwd(qn, kn, vn, dense)
+    label = f"B{B} H{Hq}/{Hkv} T{T} D{D}"
+    assert_close(out.detach(), torch.from_numpy(o_ref), ATOL, RTOL, f"out {label}")
+    assert_close(lse.detach(), torch.from_numpy(lse_ref), 1e-3, 1e-3, f"lse {label}")
+    if not bwd:
+        return
+    out.backward(do)
+    dq_ref, dk_ref, dv_ref = ao.attention_bwd(qn, kn, vn, o_ref, don, lse_ref, dense)
+    assert_close(q.grad, torch.from_numpy(dq_ref), ATOL, RTOL, f"dq {label}")
+    assert_close(k.grad, torch.from_numpy(dk_ref), ATOL, RTOL, f"dk {label}")
+    assert_close(v.grad, torch.from_numpy(dv_ref), ATOL, RTOL, f"dv {label}")
+
+
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("T", [128, 256, 1000])
+def test_doc_causal_small(T, D, gpu_device):
+    rows = [row_arrays(synth.lognormal_docs(T, 60.0, 1.0, 300, seed=T + D))]
+    _oracle_check(rows, 1, 2, 2, T, D, seed=1, device=gpu_device)
+
+
+@pytest.mark.parametrize("D", [64, 128])
+def test_cross_doc_link_small(D, gpu_device):
+    rows = [row_arrays(synth.linked_lognormal_docs(512, 50.0, 1.0, 300, 0.3, seed=3))]
+    _oracle_check(rows, 1, 2, 2, 512, D, seed=2, device=gpu_device)
+
+
+def test_gqa_and_batch_masks(gpu_device):
+    rng = np.random.default_rng(11)
+    rows = [random_row(384, rng, words=2, uncovered=True, max_doc=120) for _ in range(2)]
+    _oracle_check(rows, 2, 4, 2, 384, 64, seed=4, device=gpu_device)
+
+
+def test_ragged_uncovered_tokens(gpu_device):
+    rng = np.random.default_rng(12)
+    rows = [random_row(333, rng, words=1, uncovered=True, max_doc=90)]
+    _oracle_check(rows, 1, 2, 1, 333, 128, seed=5, device=gpu_device)
+
+
+def test_config1_shape_bf16(gpu_device):
+    rows = [row_arrays(r) for r in synth.config_rows(1, seed=0)]
+    _oracle_check(rows, 1, 4, 4, 1024, 64, seed=0, device=gpu_device)
+
+
+def test_backward_is_deterministic(gpu_device):
+    rows = [row_arrays(r) for r in synth.config_rows(3, seed=0, T=2048)]
+    bm = _mask_from_rows(rows, gpu_device)
+    q, k, v, do = _inputs(1, 4, 2, 2048, 128, 7, gpu_device)
+    grads = []
+    for _ in range(2):
+        qq, kk, vv = (t.clone().requires_grad_(True) for t in (q, k, v))
+        flex_attention(qq, kk, vv, block_mask=bm, enable_gqa=True).backward(do)
+        grads.append((qq.grad.clone(), kk.grad.clone(), vv.grad.clone()))
+    for a, b in zip(*grads):
+        assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("cfg", [2, 3, 4])
+def test_full_size_against_torch_fp32(cfg, gpu_device):
+    c = synth.CONFIGS[cfg]
+    B, Hq, Hkv, T, D = c["B"], c["Hq"], c["Hkv"], c["T"], c["D"]
+    rows = [row_arrays(r) for r in synth.config_rows(cfg, seed=0)]
+    bm = _mask_from_rows(rows, gpu_device)
+    q, k, v, do = _inputs(B, Hq, Hkv, T, D, cfg, gpu_device)
+    q.requires_grad_(True); k.requires_grad_(True); v.requires_grad_(True)
+    out = flex_attention(q, k, v, block_mask=bm, enable_gqa=Hq != Hkv)
+    out.backward(do)
+    G = Hq // Hkv
+    heads = list(range(G)) if G > 1 else [0, Hq - 1]  # a whole GQA group -> exact dk/dv
+    masks = []
+    for r in rows:
+        masks.append((torch.from_numpy(r[0]).to(gpu_device), to_dev_words(r[1], gpu_device),
+                      to_dev_words(r[2], gpu_device)))
+    ref = torch_ref_attention(q.detach(), k.detach(), v.detach(), do, masks, heads=heads)
+    for (b, h), o_ref in ref["o"].items():
+        assert_close(out[b, h].detach(), o_ref, ATOL, RTOL, f"cfg{cfg} out b{b} h{h}")
+        assert_close(q.grad[b, h], ref["dq"][(b, h)], ATOL, RTOL, f"cfg{cfg} dq b{b} h{h}")
+    # each checked KV head has all of its query heads evaluated -> complete dk / dv
+    for (b, hk), dk_ref in ref["dk"].items():
+        assert_close(k.grad[b, hk], dk_ref, ATOL, RTOL, f"cfg{cfg} dk b{b} hk{hk}")
+        assert_close(v.grad[b, hk], ref["dv"][(b, hk)], ATOL, RTOL, f"cfg{cfg} dv b{b} hk{hk}")
