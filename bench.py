@@ -1,0 +1,293 @@
+"""Benchmark of the gfx950 masked-attention hot path.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 3]
+
+One step = one pass of the hot path over one batch: the metadata pass
+(tile classification + BlockMask tables from per-token inputs), the forward
+kernel and the three backward launches, with every input already resident in
+HBM.  Prints one JSON line.
+
+metric  : BASELINE.json's "masked attn fwd+bwd useful TFLOP/s", quoted on
+          configs[2] (cross_doc_link, B1 H16 T16384 D128, bf16) by default.
+useful FLOPs per step = 14 * D * N_pairs * Hq (fwd 4, bwd 10: the FA2
+          convention), N_pairs = exact number of allowed (b, q, kv) pairs.
+roofline: the dominant kernel's algorithmic FLOPs per launch / its mean
+          duration (HIP events on the launch stream) vs the MI355X dense bf16
+          MFMA peak.
+cpu_baseline: the reference's CPU path -- torch eager flex_attention +
+          create_block_mask with the reference's mask_mod -- on a bounded
+          sample (one head), scaled to the whole step.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+from tagseq2tagseq_amd import synth  # noqa: E402
+from tagseq2tagseq_amd.attention import BwdPhases, attn_bwd, attn_fwd  # noqa: E402
+from tagseq2tagseq_amd.block_mask import build_block_mask  # noqa: E402
+
+METRIC = "masked attn fwd+bwd useful TFLOP/s + % bf16 MFMA peak, cross_doc_link T=16k"
+PEAK_BF16_TFLOPS = 2516.6   # MI355X dense bf16 MFMA: 256 CU x 2.4 GHz x 4096 FLOP/clk
+PEAK_HBM_GBS = 8000.0
+
+WORKLOAD_NAMES = {
+    2: "doc_causal fwd+bwd bf16 B2 H12 T8192 D64 (configs[1])",
+    3: "cross_doc_link fwd+bwd bf16 B1 H16 T16384 D128 (configs[2])",
+    4: "cross_doc_link GQA fwd+bwd bf16 B1 Hq16/Hkv4 T32768 D128 (configs[3])",
+}
+
+
+def per_token_arrays(row: synth.SynthRow):
+    """doc ids (span ids) and grant words of one synthetic row, host numpy."""
+    from tagseq2tagseq_amd.mask_creators import document_ids_host
+    T = row.seq_len
+    doc = document_ids_host(T, row.spans)
+    if row.link_rows is None:
+        return doc, None, None
+    W = row.link_rows.shape[1]
+    qb = np.zeros((W, T), dtype=np.uint64)
+    kb = np.zeros((W, T), dtype=np.uint64)
+    cov = row.doc_index >= 0
+    d = row.doc_index[cov].astype(np.int64)
+    qb[:, cov] = row.link_rows[d].T
+    kb[d // 64, np.nonzero(cov)[0]] = np.uint64(1) << (d % 64).astype(np.uint64)
+    return doc, qb, kb
+
+
+def count_pairs(doc, qb, kb, chunk=1024) -> int:
+    """Exact allowed-pair count of one mask row, on the GPU (chunked rows)."""
+    T = doc.shape[0]
+    total = 0
+    kv = torch.arange(T, device=doc.device)[None, :]
+    for r0 in range(0, T, chunk):
+        r1 = min(T, r0 + chunk)
+        m = doc[r0:r1, None] == doc[None, :]
+        if qb is not None:
+            for w in range(qb.shape[0]):
+                m |= (qb[w, r0:r1, None] & kb[w][None, :]) != 0
+        m &= torch.arange(r0, r1, device=doc.device)[:, None] >= kv
+        total += int(m.sum().item())
+    return total
+
+
+def time_launches(fn, reps: int) -> float:
+    """Mean duration (ms) of fn()'s launches, HIP events on the current stream."""
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    fn()
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(reps):
+        fn()
+    end.record()
+    end.synchronize()
+    return start.elapsed_time(end) / reps
+
+
+def cpu_baseline(rows_np, c, seed, threads):
+    """Reference CPU path on one head: create_block_mask + eager flex_attention
+    fwd+bwd (torch/_higher_order_ops/flex_attention.py:202-294, 825-994) with the
+    reference's mask_mod (restated in oracle/mask_oracle.py)."""
+    from oracle.mask_oracle import torch_mask_mod
+    from torch.nn.attention.flex_attention import create_block_mask, flex_attention
+    torch.set_num_threads(threads)
+    T, D = c["T"], c["D"]
+    doc, qb, kb = rows_np[0]
+    mod = torch_mask_mod(torch.from_numpy(doc),
+                         None if qb is None else torch.from_numpy(qb.view(np.int64)),
+                         None if kb is None else torch.from_numpy(kb.view(np.int64)))
+    t0 = time.perf_counter()
+    bm = create_block_mask(mod, None, None, T, T, device="cpu")
+    t_mask = time.perf_counter() - t0
+    g = torch.Generator().manual_seed(seed)
+    dt = torch.bfloat16
+    q = torch.randn(1, 1, T, D, generator=g).to(dt).requires_grad_(True)
+    k = torch.randn(1, 1, T, D, generator=g).to(dt).requires_grad_(True)
+    v = torch.randn(1, 1, T, D, generator=g).to(dt).requires_grad_(True)
+    do = torch.randn(1, 1, T, D, generator=g).to(dt)
+    t0 = time.perf_counter()
+    out = flex_attention(q, k, v, block_mask=bm)
+    out.backward(do)
+    t_head = time.perf_counter() - t0
+    n_rows = len(rows_np)
+    # Cost is linear in heads and in independent batch rows.
+    t_step = n_rows * (t_mask + c["Hq"] * t_head)
+    return t_step, t_mask, t_head
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", type=int, default=3, choices=[2, 3, 4])
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--reps", type=int, default=20, help="launches per per-kernel timing")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-threads", type=int, default=min(16, os.cpu_count() or 1))
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a 1 GiB device copy (HBM-counter calibration)")
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only: this build has no multi-GPU path "
+              f"(--gpus {args.gpus} requested)", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        sys.exit(2)
+    dev = torch.device("cuda:0")
+
+    if args.copy_calibration:
+        x = torch.empty(1 << 30, dtype=torch.uint8, device=dev).fill_(1)
+        y = torch.empty_like(x)
+        for _ in range(5):
+            y.copy_(x)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes": x.numel(), "launches": 5}))
+        return
+
+    c = synth.CONFIGS[args.config]
+    B, Hq, Hkv, T, D = c["B"], c["Hq"], c["Hkv"], c["T"], c["D"]
+    rows = synth.config_rows(args.config, seed=args.seed)
+    rows_np = [per_token_arrays(r) for r in rows]
+
+    doc = torch.stack([torch.from_numpy(r[0]) for r in rows_np]).to(dev)
+    if rows_np[0][1] is not None:
+        qb = torch.stack([torch.from_numpy(r[1].view(np.int64)) for r in rows_np]).to(dev)
+        kb = torch.stack([torch.from_numpy(r[2].view(np.int64)) for r in rows_np]).to(dev)
+    else:
+        qb = kb = None
+    g = torch.Generator().manual_seed(args.seed)
+    q = torch.randn(B, Hq, T, D, generator=g).to(torch.bfloat16).to(dev)
+    k = torch.randn(B, Hkv, T, D, generator=g).to(torch.bfloat16).to(dev)
+    v = torch.randn(B, Hkv, T, D, generator=g).to(torch.bfloat16).to(dev)
+    do = torch.randn(B, Hq, T, D, generator=g).to(torch.bfloat16).to(dev)
+    scale = 1.0 / math.sqrt(D)
+
+    n_pairs = 0
+    for b in range(B):
+        bb = b if len(rows_np) > 1 else 0
+        n_pairs += count_pairs(doc[bb], None if qb is None else qb[bb], None if kb is None else kb[bb])
+    causal_pairs = B * T * (T + 1) // 2
+    useful_flops = 14.0 * D * n_pairs * Hq
+
+    def step():
+        bm = build_block_mask(doc, qb, kb)
+        out, lse2 = attn_fwd(q, k, v, bm, scale)
+        return attn_bwd(q, k, v, out, do, lse2, bm, scale)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    ev0.record()
+    for _ in range(args.steps):
+        step()
+    ev1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_per_step = ev0.elapsed_time(ev1) / args.steps
+    value = useful_flops / (ms_per_step * 1e-3) / 1e12
+
+    # Per-kernel mean durations on fixed buffers.
+    bm = build_block_mask(doc, qb, kb)
+    out, lse2 = attn_fwd(q, k, v, bm, scale)
+    ph = BwdPhases(q, k, v, out, do, lse2, bm, scale)
+    ph.preprocess()
+    t_meta = time_launches(lambda: build_block_mask(doc, qb, kb), args.reps)
+    t_fwd = time_launches(lambda: attn_fwd(q, k, v, bm, scale), args.reps)
+    t_pre = time_launches(ph.preprocess, args.reps)
+    t_dkdv = time_launches(ph.dkdv, args.reps)
+    t_dq = time_launches(ph.dq_pass, args.reps)
+
+    base = D * n_pairs * Hq
+    kernels = {
+        "attn_fwd_bf16_kernel": (t_fwd, 4.0 * base),
+        "bwd_dkdv_kernel": (t_dkdv, 8.0 * base),
+        "bwd_dq_kernel": (t_dq, 6.0 * base),
+    }
+    dom = max(kernels, key=lambda n: kernels[n][0])
+    dom_ms, dom_flops = kernels[dom]
+    achieved = dom_flops / (dom_ms * 1e-3) / 1e12
+
+    nt = (T + 127) // 128
+    Bm = doc.shape[0]
+    W = 0 if qb is None else qb.shape[1]
+    meta_bytes = Bm * T * 4 + 2 * 8 * W * Bm * T + Bm * nt * nt + 4 * (4 * Bm * nt * nt + 4 * Bm * nt)
+    tc = bm.tile_class
+    tiles = {"full": int((tc == 2).sum()), "partial": int((tc == 1).sum()), "skip": int((tc == 0).sum())}
+
+    result = {
+        "metric": METRIC,
+        "value": round(value, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded packed documents, Q/K/V/dO ~ N(0,1))",
+        "config": {
+            "workload": WORKLOAD_NAMES[args.config],
+            "B": B, "Hq": Hq, "Hkv": Hkv, "T": T, "D": D, "seed": args.seed,
+            "n_docs": [r.n_docs for r in rows], "grant_words": W,
+            "n_pairs": n_pairs, "density_vs_causal": round(n_pairs / causal_pairs, 4),
+            "tiles_128": tiles,
+        },
+        "pct_of_bf16_peak": round(100.0 * value / PEAK_BF16_TFLOPS, 2),
+        "roofline": {
+            "bound": "mfma",
+            "kernel": dom,
+            "achieved": round(achieved, 2),
+            "peak": PEAK_BF16_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+            "traffic": None,
+        },
+        "kernels_ms": {
+            "mask_meta (2 launches)": round(t_meta, 4),
+            "attn_fwd_bf16_kernel": round(t_fwd, 4),
+            "bwd_delta_kernel": round(t_pre, 4),
+            "bwd_dkdv_kernel": round(t_dkdv, 4),
+            "bwd_dq_kernel": round(t_dq, 4),
+        },
+        "mask_meta": {"us": round(t_meta * 1e3, 2), "bytes": int(meta_bytes),
+                      "GBps": round(meta_bytes / (t_meta * 1e-3) / 1e9, 2)},
+        "wall_s_timed": round(wall, 3),
+    }
+
+    if not args.no_cpu_baseline:
+        t_step, t_mask, t_head = cpu_baseline(rows_np, c, args.seed, args.cpu_threads)
+        result["cpu_baseline"] = {
+            "value": round(useful_flops / t_step / 1e12, 6),
+            "unit": "TFLOP/s",
+            "cores": args.cpu_threads,
+            "kind": "reference",
+            "sample": (f"torch {torch.__version__} eager create_block_mask + flex_attention fwd+bwd "
+                       f"on CPU with the reference mask_mod, 1 of {Hq} heads of batch row 0 "
+                       f"(mask {t_mask:.2f} s, head {t_head:.2f} s), scaled x{Hq} heads "
+                       f"x{len(rows_np)} rows"),
+            "s_per_step": round(t_step, 2),
+        }
+    print(json.dumps(result))
+
+
+if __name__ == "__main__":
+    main()

@@ -121,6 +121,28 @@ int t2t_attn_bwd(const t2t_tensor *q, const t2t_tensor *k, const t2t_tensor *v,
                  const t2t_tensor *dv, int32_t B, int32_t Hq, int32_t Hkv, int32_t T,
                  int32_t D, int32_t dtype, float scale, const t2t_mask *mask, void *stream);
 
+/*
+ * The three phases t2t_attn_bwd runs, callable separately (for example to
+ * run dK/dV and dQ on two streams once Delta is ready).  Same conventions:
+ *   preprocess: delta[b][h][t] = sum_d o * dout       (bwd Delta, :910-914)
+ *   dkdv:       dk, dv  (KV-tile-major, walks q_num/q_idx + full_q_*)
+ *   dq:         dq      (Q-tile-major, walks kv_num/kv_idx + full_kv_*)
+ */
+int t2t_attn_bwd_preprocess(const t2t_tensor *o, const t2t_tensor *dout, float *delta,
+                            int32_t B, int32_t Hq, int32_t T, int32_t D, int32_t dtype,
+                            void *stream);
+
+int t2t_attn_bwd_dkdv(const t2t_tensor *q, const t2t_tensor *k, const t2t_tensor *v,
+                      const t2t_tensor *dout, const float *lse2, const float *delta,
+                      const t2t_tensor *dk, const t2t_tensor *dv, int32_t B, int32_t Hq,
+                      int32_t Hkv, int32_t T, int32_t D, int32_t dtype, float scale,
+                      const t2t_mask *mask, void *stream);
+
+int t2t_attn_bwd_dq(const t2t_tensor *q, const t2t_tensor *k, const t2t_tensor *v,
+                    const t2t_tensor *dout, const float *lse2, const float *delta,
+                    const t2t_tensor *dq, int32_t B, int32_t Hq, int32_t Hkv, int32_t T,
+                    int32_t D, int32_t dtype, float scale, const t2t_mask *mask, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -219,3 +219,27 @@ def block_mask_tables(doc_ids: np.ndarray, q_bits=None, kv_bits=None,
     out["q_num_blocks"], out["q_indices"] = transpose_ordered(partial)
     out["full_q_num_blocks"], out["full_q_indices"] = transpose_ordered(full)
     return out
+
+
+def torch_mask_mod(doc_ids, q_bits=None, kv_bits=None):
+    """The reference's mask_mod (cross_doc_mask.py:348-357; doc_causal_mod of
+    block_mask_creator.py:121-129 when there are no grant words) as a closure
+    over torch tensors, for torch's create_block_mask / flex_attention.
+
+    doc_ids int32 [T]; q_bits / kv_bits int64 [W, T] (uint64 bit patterns) or None.
+    """
+    W = 0 if q_bits is None else int(q_bits.shape[0])
+    q_list = [q_bits[w] for w in range(W)]
+    kv_list = [kv_bits[w] for w in range(W)]
+
+    def reference_mask_mod(b, h, q_idx, kv_idx):
+        causal = q_idx >= kv_idx
+        same_doc = doc_ids[q_idx] == doc_ids[kv_idx]
+        if W:
+            in_grant = (q_list[0][q_idx] & kv_list[0][kv_idx]) != 0
+            for i in range(1, W):
+                in_grant = in_grant | ((q_list[i][q_idx] & kv_list[i][kv_idx]) != 0)
+            return causal & (same_doc | in_grant)
+        return causal & same_doc
+
+    return reference_mask_mod

@@ -119,6 +119,53 @@ def attn_bwd(q, k, v, out, dout, lse2, block_mask: T2TBlockMask, scale: float):
     return dq, dk, dv
 
 
+class BwdPhases:
+    """The three backward launches bound to fixed buffers (t2t_attn_bwd_preprocess,
+    t2t_attn_bwd_dkdv, t2t_attn_bwd_dq), for callers that schedule or time
+    them separately."""
+
+    def __init__(self, q, k, v, out, dout, lse2, block_mask: T2TBlockMask, scale: float):
+        self.B, self.Hq, self.T, self.D = q.shape
+        self.Hkv = k.shape[1]
+        self.dq = torch.empty_like(q, memory_format=torch.contiguous_format)
+        self.dk = torch.empty_like(k, memory_format=torch.contiguous_format)
+        self.dv = torch.empty_like(v, memory_format=torch.contiguous_format)
+        self.delta = torch.empty((self.B, self.Hq, self.T), dtype=torch.float32, device=q.device)
+        self._keep = (q, k, v, out, dout, lse2, block_mask)
+        self._v = {n: _view(t) for n, t in dict(q=q, k=k, v=v, o=out, do=dout, dq=self.dq,
+                                                 dk=self.dk, dv=self.dv).items()}
+        self._lse2 = lse2.data_ptr()
+        self._mask = block_mask.c_struct()
+        self._dtype = _DTYPE_CODES[q.dtype]
+        self._scale = float(scale)
+        self._dev = q.device
+
+    def preprocess(self):
+        v = self._v
+        rc = _lib.lib().t2t_attn_bwd_preprocess(ctypes.byref(v["o"]), ctypes.byref(v["do"]),
+                                                self.delta.data_ptr(), self.B, self.Hq, self.T,
+                                                self.D, self._dtype, _stream_ptr(self.delta))
+        _lib.check(rc, "t2t_attn_bwd_preprocess")
+
+    def dkdv(self):
+        v = self._v
+        rc = _lib.lib().t2t_attn_bwd_dkdv(
+            ctypes.byref(v["q"]), ctypes.byref(v["k"]), ctypes.byref(v["v"]), ctypes.byref(v["do"]),
+            self._lse2, self.delta.data_ptr(), ctypes.byref(v["dk"]), ctypes.byref(v["dv"]),
+            self.B, self.Hq, self.Hkv, self.T, self.D, self._dtype, self._scale,
+            ctypes.byref(self._mask), _stream_ptr(self.delta))
+        _lib.check(rc, "t2t_attn_bwd_dkdv")
+
+    def dq_pass(self):
+        v = self._v
+        rc = _lib.lib().t2t_attn_bwd_dq(
+            ctypes.byref(v["q"]), ctypes.byref(v["k"]), ctypes.byref(v["v"]), ctypes.byref(v["do"]),
+            self._lse2, self.delta.data_ptr(), ctypes.byref(v["dq"]),
+            self.B, self.Hq, self.Hkv, self.T, self.D, self._dtype, self._scale,
+            ctypes.byref(self._mask), _stream_ptr(self.delta))
+        _lib.check(rc, "t2t_attn_bwd_dq")
+
+
 class T2TFlexAttentionFn(torch.autograd.Function):
     """autograd.Function over the gfx950 kernels (in place of
     FlexAttentionAutogradOp, torch/_higher_order_ops/flex_attention.py:628-767)."""

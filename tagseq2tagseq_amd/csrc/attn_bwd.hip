@@ -369,11 +369,12 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dq_kernel(BwdParams p) {
   }
 }
 
-hipError_t launch_attn_bwd_bf16(const TensorView& q, const TensorView& k, const TensorView& v,
-                                const TensorView& o, const TensorView& dout, const float* lse2,
-                                float* delta, const TensorView& dq, const TensorView& dk,
-                                const TensorView& dv, const AttnDims& dims,
-                                const MaskTables& mask, hipStream_t stream) {
+namespace {
+
+BwdParams make_bwd_params(const TensorView& q, const TensorView& k, const TensorView& v,
+                          const TensorView& o, const TensorView& dout, const float* lse2,
+                          float* delta, const TensorView& dq, const TensorView& dk,
+                          const TensorView& dv, const AttnDims& dims, const MaskTables& mask) {
   BwdParams p;
   p.q = static_cast<const __bf16*>(q.data); p.q_sb = q.sb; p.q_sh = q.sh; p.q_st = q.st;
   p.k = static_cast<const __bf16*>(k.data); p.k_sb = k.sb; p.k_sh = k.sh; p.k_st = k.st;
@@ -390,18 +391,34 @@ hipError_t launch_attn_bwd_bf16(const TensorView& q, const TensorView& k, const 
   p.scale = dims.scale;
   p.scale_log2 = dims.scale * kLog2e;
   p.m = mask;
+  return p;
+}
+
+}  // namespace
+
+hipError_t launch_attn_bwd_phase(int phase, const TensorView& q, const TensorView& k,
+                                 const TensorView& v, const TensorView& o,
+                                 const TensorView& dout, const float* lse2, float* delta,
+                                 const TensorView& dq, const TensorView& dk, const TensorView& dv,
+                                 const AttnDims& dims, const MaskTables& mask,
+                                 hipStream_t stream) {
+  const BwdParams p = make_bwd_params(q, k, v, o, dout, lse2, delta, dq, dk, dv, dims, mask);
   if (p.nt == 0 || dims.B == 0 || dims.Hq == 0) return hipSuccess;
-  const int64_t rows = (int64_t)dims.B * dims.Hq * dims.T;
-  const int rows_per_block = kThreads / (dims.D / 8);
-  const dim3 dgrid((unsigned)((rows + rows_per_block - 1) / rows_per_block));
-  if (dims.D == 64) {
-    hipLaunchKernelGGL(bwd_delta_kernel<64>, dgrid, dim3(kThreads), 0, stream, p);
-    hipLaunchKernelGGL(bwd_dkdv_kernel<64>, dim3(p.nt, dims.Hkv, dims.B), dim3(kThreads), 0, stream, p);
-    hipLaunchKernelGGL(bwd_dq_kernel<64>, dim3(p.nt, dims.Hq, dims.B), dim3(kThreads), 0, stream, p);
+  const bool d64 = dims.D == 64;
+  if (phase == kBwdDelta) {
+    const int64_t rows = (int64_t)dims.B * dims.Hq * dims.T;
+    const int rows_per_block = kThreads / (dims.D / 8);
+    const dim3 grid((unsigned)((rows + rows_per_block - 1) / rows_per_block));
+    if (d64) hipLaunchKernelGGL(bwd_delta_kernel<64>, grid, dim3(kThreads), 0, stream, p);
+    else hipLaunchKernelGGL(bwd_delta_kernel<128>, grid, dim3(kThreads), 0, stream, p);
+  } else if (phase == kBwdDkDv) {
+    const dim3 grid(p.nt, dims.Hkv, dims.B);
+    if (d64) hipLaunchKernelGGL(bwd_dkdv_kernel<64>, grid, dim3(kThreads), 0, stream, p);
+    else hipLaunchKernelGGL(bwd_dkdv_kernel<128>, grid, dim3(kThreads), 0, stream, p);
   } else {
-    hipLaunchKernelGGL(bwd_delta_kernel<128>, dgrid, dim3(kThreads), 0, stream, p);
-    hipLaunchKernelGGL(bwd_dkdv_kernel<128>, dim3(p.nt, dims.Hkv, dims.B), dim3(kThreads), 0, stream, p);
-    hipLaunchKernelGGL(bwd_dq_kernel<128>, dim3(p.nt, dims.Hq, dims.B), dim3(kThreads), 0, stream, p);
+    const dim3 grid(p.nt, dims.Hq, dims.B);
+    if (d64) hipLaunchKernelGGL(bwd_dq_kernel<64>, grid, dim3(kThreads), 0, stream, p);
+    else hipLaunchKernelGGL(bwd_dq_kernel<128>, grid, dim3(kThreads), 0, stream, p);
   }
   return hipGetLastError();
 }

@@ -45,10 +45,16 @@ hipError_t launch_attn_fwd_bf16(const TensorView& q, const TensorView& k, const 
                                 const TensorView& o, float* lse2, const AttnDims& dims,
                                 const MaskTables& mask, hipStream_t stream);
 
-hipError_t launch_attn_bwd_bf16(const TensorView& q, const TensorView& k, const TensorView& v,
-                                const TensorView& o, const TensorView& dout, const float* lse2,
-                                float* delta, const TensorView& dq, const TensorView& dk,
-                                const TensorView& dv, const AttnDims& dims,
-                                const MaskTables& mask, hipStream_t stream);
+enum BwdPhase { kBwdDelta = 0, kBwdDkDv = 1, kBwdDq = 2 };
+
+// One backward phase.  Unused views may be empty for a phase that does not
+// read them (delta: o, dout; dkdv: q, k, v, dout, lse2, delta, dk, dv; dq: q,
+// k, v, dout, lse2, delta, dq).
+hipError_t launch_attn_bwd_phase(int phase, const TensorView& q, const TensorView& k,
+                                 const TensorView& v, const TensorView& o,
+                                 const TensorView& dout, const float* lse2, float* delta,
+                                 const TensorView& dq, const TensorView& dk, const TensorView& dv,
+                                 const AttnDims& dims, const MaskTables& mask,
+                                 hipStream_t stream);
 
 }  // namespace t2t

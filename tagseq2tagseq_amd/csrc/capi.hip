@@ -118,6 +118,69 @@ int t2t_attn_fwd(const t2t_tensor* q, const t2t_tensor* k, const t2t_tensor* v,
                     "t2t_attn_fwd launch");
 }
 
+int t2t_attn_bwd_preprocess(const t2t_tensor* o, const t2t_tensor* dout, float* delta,
+                            int32_t B, int32_t Hq, int32_t T, int32_t D, int32_t dtype,
+                            void* stream) {
+  int rc = check_dims(B, Hq, Hq > 0 ? Hq : 1, T, D, dtype);
+  if (rc) return rc;
+  if (B == 0 || Hq == 0 || T == 0) return T2T_OK;
+  if (!view_ok(o) || !view_ok(dout)) return fail(T2T_EINVAL, "o/dout view invalid");
+  if (!delta) return fail(T2T_EINVAL, "delta is NULL");
+  const t2t::TensorView none{nullptr, 0, 0, 0};
+  t2t::AttnDims dims{B, Hq, Hq, T, D, 1.f};
+  t2t::MaskTables m{};
+  return hip_status(t2t::launch_attn_bwd_phase(t2t::kBwdDelta, none, none, none, as_view(o),
+                                               as_view(dout), nullptr, delta, none, none, none,
+                                               dims, m, static_cast<hipStream_t>(stream)),
+                    "t2t_attn_bwd_preprocess launch");
+}
+
+int t2t_attn_bwd_dkdv(const t2t_tensor* q, const t2t_tensor* k, const t2t_tensor* v,
+                      const t2t_tensor* dout, const float* lse2, const float* delta,
+                      const t2t_tensor* dk, const t2t_tensor* dv, int32_t B, int32_t Hq,
+                      int32_t Hkv, int32_t T, int32_t D, int32_t dtype, float scale,
+                      const t2t_mask* mask, void* stream) {
+  int rc = check_dims(B, Hq, Hkv, T, D, dtype);
+  if (rc) return rc;
+  if (B == 0 || Hq == 0 || T == 0) return T2T_OK;
+  if (!view_ok(q) || !view_ok(k) || !view_ok(v) || !view_ok(dout) || !view_ok(dk) ||
+      !view_ok(dv))
+    return fail(T2T_EINVAL, "tensor view invalid (NULL, misaligned or bad stride)");
+  if (!lse2 || !delta) return fail(T2T_EINVAL, "lse2/delta is NULL");
+  rc = check_mask(mask, B, false, true);
+  if (rc) return rc;
+  const t2t::TensorView none{nullptr, 0, 0, 0};
+  t2t::AttnDims dims{B, Hq, Hkv, T, D, scale};
+  return hip_status(t2t::launch_attn_bwd_phase(t2t::kBwdDkDv, as_view(q), as_view(k), as_view(v),
+                                               none, as_view(dout), lse2,
+                                               const_cast<float*>(delta), none, as_view(dk),
+                                               as_view(dv), dims, as_tables(mask),
+                                               static_cast<hipStream_t>(stream)),
+                    "t2t_attn_bwd_dkdv launch");
+}
+
+int t2t_attn_bwd_dq(const t2t_tensor* q, const t2t_tensor* k, const t2t_tensor* v,
+                    const t2t_tensor* dout, const float* lse2, const float* delta,
+                    const t2t_tensor* dq, int32_t B, int32_t Hq, int32_t Hkv, int32_t T,
+                    int32_t D, int32_t dtype, float scale, const t2t_mask* mask, void* stream) {
+  int rc = check_dims(B, Hq, Hkv, T, D, dtype);
+  if (rc) return rc;
+  if (B == 0 || Hq == 0 || T == 0) return T2T_OK;
+  if (!view_ok(q) || !view_ok(k) || !view_ok(v) || !view_ok(dout) || !view_ok(dq))
+    return fail(T2T_EINVAL, "tensor view invalid (NULL, misaligned or bad stride)");
+  if (!lse2 || !delta) return fail(T2T_EINVAL, "lse2/delta is NULL");
+  rc = check_mask(mask, B, true, false);
+  if (rc) return rc;
+  const t2t::TensorView none{nullptr, 0, 0, 0};
+  t2t::AttnDims dims{B, Hq, Hkv, T, D, scale};
+  return hip_status(t2t::launch_attn_bwd_phase(t2t::kBwdDq, as_view(q), as_view(k), as_view(v),
+                                               none, as_view(dout), lse2,
+                                               const_cast<float*>(delta), as_view(dq), none,
+                                               none, dims, as_tables(mask),
+                                               static_cast<hipStream_t>(stream)),
+                    "t2t_attn_bwd_dq launch");
+}
+
 int t2t_attn_bwd(const t2t_tensor* q, const t2t_tensor* k, const t2t_tensor* v,
                  const t2t_tensor* o, const t2t_tensor* dout, const float* lse2,
                  float* delta, const t2t_tensor* dq, const t2t_tensor* dk,
@@ -126,18 +189,14 @@ int t2t_attn_bwd(const t2t_tensor* q, const t2t_tensor* k, const t2t_tensor* v,
   int rc = check_dims(B, Hq, Hkv, T, D, dtype);
   if (rc) return rc;
   if (B == 0 || Hq == 0 || T == 0) return T2T_OK;
-  if (!view_ok(q) || !view_ok(k) || !view_ok(v) || !view_ok(o) || !view_ok(dout) ||
-      !view_ok(dq) || !view_ok(dk) || !view_ok(dv))
-    return fail(T2T_EINVAL, "tensor view invalid (NULL, misaligned or bad stride)");
-  if (!lse2 || !delta) return fail(T2T_EINVAL, "lse2/delta is NULL");
-  rc = check_mask(mask, B, true, true);
+  if (!view_ok(o)) return fail(T2T_EINVAL, "o view invalid");
+  rc = t2t_attn_bwd_preprocess(o, dout, delta, B, Hq, T, D, dtype, stream);
   if (rc) return rc;
-  t2t::AttnDims dims{B, Hq, Hkv, T, D, scale};
-  return hip_status(
-      t2t::launch_attn_bwd_bf16(as_view(q), as_view(k), as_view(v), as_view(o), as_view(dout),
-                                lse2, delta, as_view(dq), as_view(dk), as_view(dv), dims,
-                                as_tables(mask), static_cast<hipStream_t>(stream)),
-      "t2t_attn_bwd launch");
+  rc = t2t_attn_bwd_dkdv(q, k, v, dout, lse2, delta, dk, dv, B, Hq, Hkv, T, D, dtype, scale,
+                         mask, stream);
+  if (rc) return rc;
+  return t2t_attn_bwd_dq(q, k, v, dout, lse2, delta, dq, B, Hq, Hkv, T, D, dtype, scale, mask,
+                         stream);
 }
 
 }  // extern "C"
