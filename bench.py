@@ -227,9 +227,13 @@ def main():
     nt = (T + 127) // 128
     Bm = doc.shape[0]
     W = 0 if qb is None else qb.shape[1]
-    meta_bytes = Bm * T * 4 + 2 * 8 * W * Bm * T + Bm * nt * nt + 4 * (4 * Bm * nt * nt + 4 * Bm * nt)
     tc = bm.tile_class
     tiles = {"full": int((tc == 2).sum()), "partial": int((tc == 1).sum()), "skip": int((tc == 0).sum())}
+    # metadata pass, algorithmic bytes: per-token reads + every table written once
+    meta_bytes = (Bm * T * 4 + 2 * 8 * W * Bm * T          # doc ids, q / kv grant words
+                  + Bm * nt * nt                           # tile classes
+                  + 4 * (5 * Bm * nt * nt + 7 * Bm * nt)   # 4 index + q_bits_slot, 4 counts + 3
+                  + 4096 * tiles["partial"])               # two 128x128-bit maps per partial tile
 
     result = {
         "metric": METRIC,
@@ -262,7 +266,7 @@ def main():
             "traffic": None,
         },
         "kernels_ms": {
-            "mask_meta (2 launches)": round(t_meta, 4),
+            "mask_meta (4 launches)": round(t_meta, 4),
             "attn_fwd_bf16_kernel": round(t_fwd, 4),
             "bwd_delta_kernel": round(t_pre, 4),
             "bwd_dkdv_kernel": round(t_dkdv, 4),

@@ -36,11 +36,14 @@ extern "C" {
 #define T2T_TILE 128   /* BlockMask tile edge (torch/nn/attention/flex_attention.py:395) */
 #define T2T_MAX_WORDS 8
 
-/* Tile classes in tile_class[]: matches torch's partial / full int8 grids
+/* Tile classes in tile_class[]: torch's partial / full int8 grids
  * (torch/nn/attention/flex_attention.py:1014-1018) folded into one byte. */
 #define T2T_TILE_SKIP 0
 #define T2T_TILE_PARTIAL 1
 #define T2T_TILE_FULL 2
+
+/* Words of one tile bitmap: [2][128][4] uint32 (row-major then column-major). */
+#define T2T_TILE_BITS_WORDS 1024
 
 /* [B, H, T, D] tensor with unit stride along D; strides in elements. */
 typedef struct t2t_tensor {
@@ -50,26 +53,42 @@ typedef struct t2t_tensor {
   int64_t stride_t;
 } t2t_tensor;
 
-/* Mask inputs plus the eight BlockMask tables (nt = ceil(T / 128)):
- * *_num int32[Bm][nt], *_idx int32[Bm][nt][nt].  Field meanings follow
+/*
+ * Block-sparse mask tables, nt = ceil(T / 128).  The first eight match
  * torch's BlockMask (kv_num_blocks, kv_indices, full_kv_num_blocks,
- * full_kv_indices, q_num_blocks, q_indices, full_q_num_blocks, full_q_indices)
- * with the head dimension dropped. */
-typedef struct t2t_mask {
-  const int32_t *doc;
-  const uint64_t *q_bits;
-  const uint64_t *kv_bits;
-  int32_t words;
+ * full_kv_indices, q_num_blocks, q_indices, full_q_num_blocks, full_q_indices;
+ * torch/nn/attention/flex_attention.py:586-657) with the head dimension
+ * dropped: *_num int32[Bm][nt], *_idx int32[Bm][nt][nt].  The rest are this
+ * library's additions:
+ *   row_order / col_order int32[Bm][nt]: tile rows / columns by descending
+ *       count of non-skip tiles (launch order for load balance);
+ *   kv_bits_off int32[Bm][nt]: bitmap slot of the first partial tile of a
+ *       row (the i-th partial tile of row r uses slot kv_bits_off[r] + i);
+ *   q_bits_slot int32[Bm][nt][nt]: bitmap slot of the i-th partial tile of a
+ *       column;
+ *   tile_bits uint32[tile_bits_slots][2][128][4]: per partial tile, the
+ *       allowed pairs as bits -- [0][q][w] bit j = allowed(q0 + q, k0 + 32 w + j),
+ *       [1][k][w] bit j = allowed(q0 + 32 w + j, k0 + k);
+ *   tile_bits_slots: capacity; Bm * nt * (nt + 1) / 2 always suffices.
+ */
+typedef struct t2t_block_mask {
   int32_t mask_batch; /* Bm */
-  const int32_t *kv_num;
-  const int32_t *kv_idx;
-  const int32_t *full_kv_num;
-  const int32_t *full_kv_idx;
-  const int32_t *q_num;
-  const int32_t *q_idx;
-  const int32_t *full_q_num;
-  const int32_t *full_q_idx;
-} t2t_mask;
+  int32_t num_tiles;  /* nt */
+  int32_t *kv_num;
+  int32_t *kv_idx;
+  int32_t *full_kv_num;
+  int32_t *full_kv_idx;
+  int32_t *q_num;
+  int32_t *q_idx;
+  int32_t *full_q_num;
+  int32_t *full_q_idx;
+  int32_t *row_order;
+  int32_t *col_order;
+  int32_t *kv_bits_off;
+  int32_t *q_bits_slot;
+  uint32_t *tile_bits;
+  int64_t tile_bits_slots;
+} t2t_block_mask;
 
 /* Library version string (host memory, static). */
 const char *t2t_version(void);
@@ -78,19 +97,19 @@ const char *t2t_version(void);
 const char *t2t_last_error(void);
 
 /*
- * Tile classification + ordered index lists of a BlockMask.
+ * Metadata pass: tile classification, the BlockMask tables and the partial
+ * tile bitmaps, written into the buffers `out` points at.
  * Replaces create_block_mask(mask_mod, B=None, H=None, T, T)
  * (torch/nn/attention/flex_attention.py:1144-1225) as called by
  * create_doc_causal_block_mask (model/graph_traversal/block_mask_creator.py:132-139)
  * and CrossDocLinkMaskCreator.__call__ (model/graph_traversal/cross_doc_mask.py:359-366),
  * without materialising the [T, T] mask.
- * Outputs: tile_class int8[Bm][nt][nt] and the eight tables of t2t_mask.
+ * tile_class: int8[Bm][nt][nt] out.  out->mask_batch / num_tiles must equal
+ * mask_batch / ceil(T / 128).
  */
 int t2t_mask_meta(const int32_t *doc, const uint64_t *q_bits, const uint64_t *kv_bits,
                   int32_t mask_batch, int32_t T, int32_t words, int8_t *tile_class,
-                  int32_t *kv_num, int32_t *kv_idx, int32_t *full_kv_num,
-                  int32_t *full_kv_idx, int32_t *q_num, int32_t *q_idx,
-                  int32_t *full_q_num, int32_t *full_q_idx, void *stream);
+                  const t2t_block_mask *out, void *stream);
 
 /*
  * Masked attention forward.  Replaces the flex_attention forward
@@ -104,7 +123,7 @@ int t2t_mask_meta(const int32_t *doc, const uint64_t *q_bits, const uint64_t *kv
  */
 int t2t_attn_fwd(const t2t_tensor *q, const t2t_tensor *k, const t2t_tensor *v,
                  const t2t_tensor *o, float *lse2, int32_t B, int32_t Hq, int32_t Hkv,
-                 int32_t T, int32_t D, int32_t dtype, float scale, const t2t_mask *mask,
+                 int32_t T, int32_t D, int32_t dtype, float scale, const t2t_block_mask *mask,
                  void *stream);
 
 /*
@@ -119,12 +138,13 @@ int t2t_attn_bwd(const t2t_tensor *q, const t2t_tensor *k, const t2t_tensor *v,
                  const t2t_tensor *o, const t2t_tensor *dout, const float *lse2,
                  float *delta, const t2t_tensor *dq, const t2t_tensor *dk,
                  const t2t_tensor *dv, int32_t B, int32_t Hq, int32_t Hkv, int32_t T,
-                 int32_t D, int32_t dtype, float scale, const t2t_mask *mask, void *stream);
+                 int32_t D, int32_t dtype, float scale, const t2t_block_mask *mask,
+                 void *stream);
 
 /*
  * The three phases t2t_attn_bwd runs, callable separately (for example to
  * run dK/dV and dQ on two streams once Delta is ready).  Same conventions:
- *   preprocess: delta[b][h][t] = sum_d o * dout       (bwd Delta, :910-914)
+ *   preprocess: delta[b][h][t] = sum_d o * dout  (sdpa_dense_backward :910-914)
  *   dkdv:       dk, dv  (KV-tile-major, walks q_num/q_idx + full_q_*)
  *   dq:         dq      (Q-tile-major, walks kv_num/kv_idx + full_kv_*)
  */
@@ -136,12 +156,13 @@ int t2t_attn_bwd_dkdv(const t2t_tensor *q, const t2t_tensor *k, const t2t_tensor
                       const t2t_tensor *dout, const float *lse2, const float *delta,
                       const t2t_tensor *dk, const t2t_tensor *dv, int32_t B, int32_t Hq,
                       int32_t Hkv, int32_t T, int32_t D, int32_t dtype, float scale,
-                      const t2t_mask *mask, void *stream);
+                      const t2t_block_mask *mask, void *stream);
 
 int t2t_attn_bwd_dq(const t2t_tensor *q, const t2t_tensor *k, const t2t_tensor *v,
                     const t2t_tensor *dout, const float *lse2, const float *delta,
                     const t2t_tensor *dq, int32_t B, int32_t Hq, int32_t Hkv, int32_t T,
-                    int32_t D, int32_t dtype, float scale, const t2t_mask *mask, void *stream);
+                    int32_t D, int32_t dtype, float scale, const t2t_block_mask *mask,
+                    void *stream);
 
 #ifdef __cplusplus
 }

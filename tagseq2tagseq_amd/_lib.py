@@ -18,6 +18,7 @@ T2T_OK = 0
 T2T_DTYPE_BF16 = 0
 TILE = 128
 MAX_WORDS = 8
+TILE_BITS_WORDS = 1024  # uint32 per tile bitmap slot ([2][128][4])
 
 
 class T2TTensor(ctypes.Structure):
@@ -25,14 +26,13 @@ class T2TTensor(ctypes.Structure):
                 ("stride_h", ctypes.c_int64), ("stride_t", ctypes.c_int64)]
 
 
-class T2TMask(ctypes.Structure):
-    _fields_ = [("doc", ctypes.c_void_p), ("q_bits", ctypes.c_void_p),
-                ("kv_bits", ctypes.c_void_p), ("words", ctypes.c_int32),
-                ("mask_batch", ctypes.c_int32),
-                ("kv_num", ctypes.c_void_p), ("kv_idx", ctypes.c_void_p),
-                ("full_kv_num", ctypes.c_void_p), ("full_kv_idx", ctypes.c_void_p),
-                ("q_num", ctypes.c_void_p), ("q_idx", ctypes.c_void_p),
-                ("full_q_num", ctypes.c_void_p), ("full_q_idx", ctypes.c_void_p)]
+class T2TBlockMaskC(ctypes.Structure):
+    """struct t2t_block_mask (include/t2t_attn.h)."""
+    _fields_ = [("mask_batch", ctypes.c_int32), ("num_tiles", ctypes.c_int32)] + [
+        (name, ctypes.c_void_p) for name in (
+            "kv_num", "kv_idx", "full_kv_num", "full_kv_idx", "q_num", "q_idx",
+            "full_q_num", "full_q_idx", "row_order", "col_order", "kv_bits_off",
+            "q_bits_slot", "tile_bits")] + [("tile_bits_slots", ctypes.c_int64)]
 
 
 _lib = None
@@ -42,7 +42,7 @@ _I32 = ctypes.c_int32
 _SIGS = {
     "t2t_version": ([], ctypes.c_char_p),
     "t2t_last_error": ([], ctypes.c_char_p),
-    "t2t_mask_meta": ([_P, _P, _P, _I32, _I32, _I32] + [_P] * 9 + [_P], ctypes.c_int),
+    "t2t_mask_meta": ([_P, _P, _P, _I32, _I32, _I32, _P, _P, _P], ctypes.c_int),
     "t2t_attn_fwd": ([_P] * 5 + [_I32] * 6 + [ctypes.c_float, _P, _P], ctypes.c_int),
     "t2t_attn_bwd": ([_P] * 10 + [_I32] * 6 + [ctypes.c_float, _P, _P], ctypes.c_int),
     "t2t_attn_bwd_preprocess": ([_P] * 3 + [_I32] * 5 + [_P], ctypes.c_int),

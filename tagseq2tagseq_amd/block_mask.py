@@ -7,8 +7,10 @@ cross_doc_mask.py:348-357) together with the BlockMask tables torch's
 1144-1225): 128 x 128 tile classes and the eight ordered index tables
 (kv_num_blocks, kv_indices, full_kv_num_blocks, full_kv_indices, q_num_blocks,
 q_indices, full_q_num_blocks, full_q_indices; shapes [Bm, 1, nt] and
-[Bm, 1, nt, nt] as in torch's BlockMask).  The tables are computed on the GPU
-by ``t2t_mask_meta`` without materialising the [T, T] mask.
+[Bm, 1, nt, nt] as in torch's BlockMask).  The metadata kernel computes them on
+the GPU without materialising the [T, T] mask, plus launch orders and a
+128 x 128 allowed-pair bitmap per partial tile that the attention kernels use
+for element masking.
 
 ``to_block_mask()`` rebuilds a torch ``BlockMask`` from the same tables (via
 ``BlockMask.from_kv_blocks``) for interoperability with torch's own
@@ -42,8 +44,13 @@ class T2TBlockMask:
     q_indices: torch.Tensor
     full_q_num_blocks: torch.Tensor
     full_q_indices: torch.Tensor
+    row_order: torch.Tensor        # int32 [Bm, nt]
+    col_order: torch.Tensor        # int32 [Bm, nt]
+    kv_bits_off: torch.Tensor      # int32 [Bm, nt]
+    q_bits_slot: torch.Tensor      # int32 [Bm, nt, nt]
+    tile_bits: torch.Tensor        # int32 [slots, 2, 128, 4]
     BLOCK_SIZE: tuple = (TILE, TILE)
-    _c: Optional[_lib.T2TMask] = field(default=None, repr=False)
+    _c: Optional[_lib.T2TBlockMaskC] = field(default=None, repr=False)
 
     @property
     def mask_batch(self) -> int:
@@ -65,18 +72,13 @@ class T2TBlockMask:
     def seq_lengths(self):
         return (self.seq_len, self.seq_len)
 
-    def c_struct(self) -> _lib.T2TMask:
+    def c_struct(self) -> _lib.T2TBlockMaskC:
         if self._c is None:
-            w = self.words
-            self._c = _lib.T2TMask(
-                self.doc_ids.data_ptr(),
-                self.q_bits.data_ptr() if w else None,
-                self.kv_bits.data_ptr() if w else None,
-                w, self.mask_batch,
-                self.kv_num_blocks.data_ptr(), self.kv_indices.data_ptr(),
-                self.full_kv_num_blocks.data_ptr(), self.full_kv_indices.data_ptr(),
-                self.q_num_blocks.data_ptr(), self.q_indices.data_ptr(),
-                self.full_q_num_blocks.data_ptr(), self.full_q_indices.data_ptr())
+            self._c = _c_struct(self.mask_batch, self.num_tiles, self.kv_num_blocks,
+                                self.kv_indices, self.full_kv_num_blocks, self.full_kv_indices,
+                                self.q_num_blocks, self.q_indices, self.full_q_num_blocks,
+                                self.full_q_indices, self.row_order, self.col_order,
+                                self.kv_bits_off, self.q_bits_slot, self.tile_bits)
         return self._c
 
     def mask_mod(self):
@@ -106,6 +108,12 @@ class T2TBlockMask:
         """Percentage of tiles that are skipped (torch BlockMask.sparsity)."""
         tc = self.tile_class
         return 100.0 * float((tc == 0).sum().item()) / max(1, tc.numel())
+
+
+def _c_struct(Bm, nt, *tensors) -> _lib.T2TBlockMaskC:
+    ptrs = [t.data_ptr() for t in tensors]
+    tile_bits = tensors[-1]
+    return _lib.T2TBlockMaskC(Bm, nt, *ptrs, tile_bits.shape[0])
 
 
 def _as_words(bits: Optional[torch.Tensor], Bm: int, T: int, device) -> torch.Tensor:
@@ -145,24 +153,31 @@ def build_block_mask(doc_ids: torch.Tensor, q_bits: Optional[torch.Tensor] = Non
     nt = (T + TILE - 1) // TILE
     i32 = dict(dtype=torch.int32, device=device)
     tile_class = torch.empty((Bm, nt, nt), dtype=torch.int8, device=device)
-    tabs = {}
+    t = {}
     for name in ("kv", "full_kv", "q", "full_q"):
-        tabs[name + "_num"] = torch.empty((Bm, 1, nt), **i32)
-        tabs[name + "_idx"] = torch.empty((Bm, 1, nt, nt), **i32)
+        t[name + "_num"] = torch.empty((Bm, 1, nt), **i32)
+        t[name + "_idx"] = torch.empty((Bm, 1, nt, nt), **i32)
+    row_order = torch.empty((Bm, nt), **i32)
+    col_order = torch.empty((Bm, nt), **i32)
+    kv_bits_off = torch.empty((Bm, nt), **i32)
+    q_bits_slot = torch.empty((Bm, nt, nt), **i32)
+    slots = max(1, Bm * nt * (nt + 1) // 2)
+    tile_bits = torch.empty((slots, 2, TILE, 4), **i32)
+    tabs = (t["kv_num"], t["kv_idx"], t["full_kv_num"], t["full_kv_idx"], t["q_num"], t["q_idx"],
+            t["full_q_num"], t["full_q_idx"], row_order, col_order, kv_bits_off, q_bits_slot,
+            tile_bits)
+    cs = _c_struct(Bm, nt, *tabs)
     s = stream if stream is not None else torch.cuda.current_stream(device)
     with torch.cuda.device(device):
         rc = _lib.lib().t2t_mask_meta(
             doc_ids.data_ptr(), qb.data_ptr() if W else None, kb.data_ptr() if W else None,
-            Bm, T, W, tile_class.data_ptr(),
-            tabs["kv_num"].data_ptr(), tabs["kv_idx"].data_ptr(),
-            tabs["full_kv_num"].data_ptr(), tabs["full_kv_idx"].data_ptr(),
-            tabs["q_num"].data_ptr(), tabs["q_idx"].data_ptr(),
-            tabs["full_q_num"].data_ptr(), tabs["full_q_idx"].data_ptr(),
-            ctypes.c_void_p(s.cuda_stream))
+            Bm, T, W, tile_class.data_ptr(), ctypes.byref(cs), ctypes.c_void_p(s.cuda_stream))
     _lib.check(rc, "t2t_mask_meta")
     return T2TBlockMask(
         seq_len=T, doc_ids=doc_ids, q_bits=qb, kv_bits=kb, tile_class=tile_class,
-        kv_num_blocks=tabs["kv_num"], kv_indices=tabs["kv_idx"],
-        full_kv_num_blocks=tabs["full_kv_num"], full_kv_indices=tabs["full_kv_idx"],
-        q_num_blocks=tabs["q_num"], q_indices=tabs["q_idx"],
-        full_q_num_blocks=tabs["full_q_num"], full_q_indices=tabs["full_q_idx"])
+        kv_num_blocks=t["kv_num"], kv_indices=t["kv_idx"],
+        full_kv_num_blocks=t["full_kv_num"], full_kv_indices=t["full_kv_idx"],
+        q_num_blocks=t["q_num"], q_indices=t["q_idx"],
+        full_q_num_blocks=t["full_q_num"], full_q_indices=t["full_q_idx"],
+        row_order=row_order, col_order=col_order, kv_bits_off=kv_bits_off,
+        q_bits_slot=q_bits_slot, tile_bits=tile_bits, _c=cs)

@@ -22,8 +22,6 @@ namespace t2t {
 
 namespace {
 
-constexpr float kLog2e = 1.4426950408889634f;
-
 struct BwdParams {
   const __bf16* q; int64_t q_sb, q_sh, q_st;
   const __bf16* k; int64_t k_sb, k_sh, k_st;
@@ -35,32 +33,10 @@ struct BwdParams {
   __bf16* dv; int64_t dv_sb, dv_sh, dv_st;
   const float* lse2;  // [B][Hq][T], log2 domain of scaled scores
   float* delta;       // [B][Hq][T]
-  int B, Hq, Hkv, T, nt;
+  int B, Hq, Hkv, T;
   float scale, scale_log2;
   MaskTables m;
 };
-
-template <int D, int PITCH>
-__device__ __forceinline__ void load_tile(__bf16* dst, const __bf16* src, int64_t st, int t0,
-                                          int T, int tid) {
-  constexpr int kChunks = D / 8;
-  constexpr int kIters = kTile * kChunks / kThreads;
-  uint4 buf[kIters];
-#pragma unroll
-  for (int it = 0; it < kIters; ++it) {
-    const int c = tid + it * kThreads;
-    const int r = c / kChunks, col = (c % kChunks) * 8;
-    const int t = t0 + r;
-    buf[it] = (t < T) ? *reinterpret_cast<const uint4*>(src + (int64_t)t * st + col)
-                      : make_uint4(0, 0, 0, 0);
-  }
-#pragma unroll
-  for (int it = 0; it < kIters; ++it) {
-    const int c = tid + it * kThreads;
-    const int r = c / kChunks, col = (c % kChunks) * 8;
-    *reinterpret_cast<uint4*>(dst + r * PITCH + col) = buf[it];
-  }
-}
 
 // Stores a transposed 32 x 32 f32 accumulator block (rows = d, cols = token)
 // scaled by `mul` as bf16 into out[token][d0 + d].
@@ -77,7 +53,7 @@ __device__ __forceinline__ void store_acc_t(__bf16* out_row, const f32x16& acc, 
 
 }  // namespace
 
-// Delta[b, h, t] = sum_d O * dO.  16 lanes per row, 8 d-values per lane.
+// Delta[b, h, t] = sum_d O * dO.  D/8 lanes per row, 8 d-values per lane.
 template <int D>
 __global__ __launch_bounds__(kThreads) void bwd_delta_kernel(BwdParams p) {
   constexpr int kLanesPerRow = D / 8;
@@ -103,31 +79,33 @@ __global__ __launch_bounds__(kThreads) void bwd_delta_kernel(BwdParams p) {
 
 template <int D>
 struct DkdvSmem {
-  static constexpr int kPitch = D + 8;
-  __bf16 q[kTile * kPitch];
-  __bf16 dout[kTile * kPitch];
+  __bf16 q[kTile * D];     // swizzled rows (lds_off)
+  __bf16 dout[kTile * D];
   float lse2[kTile];
   float delta[kTile];
-  int32_t qdoc[kTile];
-  uint64_t qbits[kMaxWords][kTile];
 };
 
+// dK, dV for one (b, kv head, 128-key tile).  Per wave 32 keys; S = Q K^T and
+// dP = dO V^T put the key in the lane and the query in the accumulator rows,
+// so P and dS feed dV^T += dO^T P and dK^T += Q^T dS directly as B operands.
 template <int D>
 __global__ __launch_bounds__(kThreads, 1) void bwd_dkdv_kernel(BwdParams p) {
-  constexpr int PITCH = DkdvSmem<D>::kPitch;
   constexpr int KS = D / 16;
   constexpr int DT = D / 32;
   __shared__ DkdvSmem<D> sm;
 
-  const int kt = blockIdx.x, hk = blockIdx.y, b = blockIdx.z;
+  const int hk = blockIdx.x, b = blockIdx.z;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int g = lane >> 5, n = lane & 31;
   const int G = p.Hq / p.Hkv;
   const int mb = p.m.Bm > 1 ? b : 0;
-  const int T = p.T, nt = p.nt, words = p.m.words;
+  const int T = p.T, nt = p.m.nt;
+  const int kt = uniform(p.m.col_order[(size_t)mb * nt + blockIdx.y]);
   const int k0 = kt * kTile;
-  const int key = k0 + 32 * wave + n;
+  const int kloc = 32 * wave + n;
+  const int key = k0 + kloc;
   const bool kvalid = key < T;
+  const float c = p.scale_log2;
 
   // K and V as the B operand (k = d, n = key): lane (g, n) holds row `key`.
   bf16x8 kf[KS], vf[KS];
@@ -138,24 +116,19 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkdv_kernel(BwdParams p) {
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
       const bf16x8 a = *reinterpret_cast<const bf16x8*>(kp + 16 * s + 8 * g);
-      const bf16x8 c = *reinterpret_cast<const bf16x8*>(vp + 16 * s + 8 * g);
+      const bf16x8 cc = *reinterpret_cast<const bf16x8*>(vp + 16 * s + 8 * g);
       kf[s] = kvalid ? a : bf16x8{};
-      vf[s] = kvalid ? c : bf16x8{};
+      vf[s] = kvalid ? cc : bf16x8{};
     }
   }
-  const int32_t* mdoc = p.m.doc + (size_t)mb * T;
-  const uint64_t* mqb = p.m.qbits + (size_t)mb * words * T;
-  const uint64_t* mkb = p.m.kvbits + (size_t)mb * words * T;
-  const int32_t kdoc = kvalid ? mdoc[key] : 0;
-  uint64_t kbits[kMaxWords];
-#pragma unroll
-  for (int w = 0; w < kMaxWords; ++w) kbits[w] = (w < words && kvalid) ? mkb[(size_t)w * T + key] : 0ull;
 
   const size_t col = (size_t)mb * nt + kt;
-  const int npart = p.m.q_num[col];
-  const int nfull = p.m.full_q_num[col];
+  const int npart = uniform(p.m.q_num[col]);
+  const int nfull = uniform(p.m.full_q_num[col]);
   const int32_t* pidx = p.m.q_idx + col * nt;
   const int32_t* fidx = p.m.full_q_idx + col * nt;
+  const int32_t* pslot = p.m.q_bits_slot + col * nt;
+  const uint32_t* bits_col = p.m.tile_bits + kTile * 4 + kloc * 4;
 
   f32x16 dkacc[DT], dvacc[DT];
 #pragma unroll
@@ -163,56 +136,57 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkdv_kernel(BwdParams p) {
 
   for (int hh = 0; hh < G; ++hh) {
     const int h = hk * G + hh;
-    const __bf16* qbase = p.q + b * p.q_sb + h * p.q_sh;
-    const __bf16* dobase = p.dout + b * p.do_sb + h * p.do_sh;
+    const auto qrs = slice_rsrc(p.q + b * p.q_sb + h * p.q_sh, p.q_st, T, D);
+    const auto dors = slice_rsrc(p.dout + b * p.do_sb + h * p.do_sh, p.do_st, T, D);
     const float* lrow = p.lse2 + ((size_t)b * p.Hq + h) * T;
     const float* drow = p.delta + ((size_t)b * p.Hq + h) * T;
     for (int it = 0; it < npart + nfull; ++it) {
       const bool partial = it < npart;
-      const int qt = partial ? pidx[it] : fidx[it - npart];
+      const int qt = uniform(partial ? pidx[it] : fidx[it - npart]);
       const int q0 = qt * kTile;
+      uint4 mbits = make_uint4(~0u, ~0u, ~0u, ~0u);
+      if (partial)
+        mbits = *reinterpret_cast<const uint4*>(bits_col + (size_t)uniform(pslot[it]) * kTileBitsWords);
       __syncthreads();
-      load_tile<D, PITCH>(sm.q, qbase, p.q_st, q0, T, tid);
-      load_tile<D, PITCH>(sm.dout, dobase, p.do_st, q0, T, tid);
+      load_tile_lds<D>(sm.q, qrs, p.q_st, q0, tid);
+      load_tile_lds<D>(sm.dout, dors, p.do_st, q0, tid);
       if (tid < kTile) {
         const int t = q0 + tid;
         const float l = t < T ? lrow[t] : -INFINITY;
         // Fully masked rows (LSE = -inf) carry P = 0: park them at +inf so
-        // exp2(s - lse) vanishes.
+        // exp2(s * c - lse) vanishes.
         sm.lse2[tid] = (l == -INFINITY) ? INFINITY : l;
         sm.delta[tid] = t < T ? drow[t] : 0.f;
-        if (partial) {
-          sm.qdoc[tid] = t < T ? mdoc[t] : 0;
-          for (int w = 0; w < words; ++w) sm.qbits[w][tid] = t < T ? mqb[(size_t)w * T + t] : 0ull;
-        }
       }
       __syncthreads();
+      const uint32_t w4[4] = {mbits.x, mbits.y, mbits.z, mbits.w};
 
-#pragma unroll 1
-      for (int qs = 0; qs < 4; ++qs) {
-        // S and dP for 32 queries x this wave's 32 keys.
-        f32x16 sacc = f32x16{}, dpacc = f32x16{};
 #pragma unroll
-        for (int s = 0; s < KS; ++s) {
-          const bf16x8 qa = lds_row8(&sm.q[(32 * qs + n) * PITCH + 16 * s + 8 * g]);
-          const bf16x8 da = lds_row8(&sm.dout[(32 * qs + n) * PITCH + 16 * s + 8 * g]);
+      for (int qs = 0; qs < 4; ++qs) {
+        // 32 queries x this wave's 32 keys: empty blocks are skipped, mixed
+        // blocks are masked through the accumulator seed (full tiles carry
+        // all-ones words).
+        if (__ballot(w4[qs] != 0u) == 0ull) continue;
+        const bool mixed = __ballot(w4[qs] != ~0u) != 0ull;
+        f32x16 sacc, dpacc;
+        {
+          const bf16x8 qa = lds_row8<D>(sm.q, 32 * qs + n, 8 * g);
+          const bf16x8 da = lds_row8<D>(sm.dout, 32 * qs + n, 8 * g);
+          if (mixed) sacc = mfma32(qa, kf[0], mask_bias(w4[qs] >> (4 * g)));
+          else sacc = mfma32(qa, kf[0], f32x16{});
+          dpacc = mfma32(da, vf[0], f32x16{});
+        }
+#pragma unroll
+        for (int s = 1; s < KS; ++s) {
+          const bf16x8 qa = lds_row8<D>(sm.q, 32 * qs + n, 16 * s + 8 * g);
+          const bf16x8 da = lds_row8<D>(sm.dout, 32 * qs + n, 16 * s + 8 * g);
           sacc = mfma32(qa, kf[s], sacc);
           dpacc = mfma32(da, vf[s], dpacc);
         }
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
           const int qq = 32 * qs + acc_row(i, g);
-          const int qrow = q0 + qq;
-          float pv = fast_exp2(sacc[i] * p.scale_log2 - sm.lse2[qq]);
-          if (partial) {
-            bool ok = kvalid && qrow < T && key <= qrow;
-            if (ok && sm.qdoc[qq] != kdoc) {
-              bool hit = false;
-              for (int w = 0; w < words; ++w) hit |= (sm.qbits[w][qq] & kbits[w]) != 0ull;
-              ok = hit;
-            }
-            if (!ok) pv = 0.f;
-          }
+          const float pv = fast_exp2(fmaf(sacc[i], c, -sm.lse2[qq]));
           sacc[i] = pv;                                  // P
           dpacc[i] = pv * (dpacc[i] - sm.delta[qq]);     // dS
         }
@@ -223,8 +197,8 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkdv_kernel(BwdParams p) {
           const bf16x8 sb = pack_half(dpacc, h2);
 #pragma unroll
           for (int dt = 0; dt < DT; ++dt) {
-            const bf16x8 doa = lds_col8(sm.dout, PITCH, 32 * qs + 16 * h2, 8, 32 * dt, lane);
-            const bf16x8 qa = lds_col8(sm.q, PITCH, 32 * qs + 16 * h2, 8, 32 * dt, lane);
+            const bf16x8 doa = lds_col8<D>(sm.dout, 32 * qs + 16 * h2, 8, 32 * dt, lane);
+            const bf16x8 qa = lds_col8<D>(sm.q, 32 * qs + 16 * h2, 8, 32 * dt, lane);
             dvacc[dt] = mfma32(doa, pb, dvacc[dt]);
             dkacc[dt] = mfma32(qa, sb, dkacc[dt]);
           }
@@ -246,29 +220,30 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkdv_kernel(BwdParams p) {
 
 template <int D>
 struct DqSmem {
-  static constexpr int kPitch = D + 8;
-  __bf16 k[kTile * kPitch];
-  __bf16 v[kTile * kPitch];
-  int32_t kdoc[kTile];
-  uint64_t kbits[kMaxWords][kTile];
+  __bf16 k[kTile * D];  // swizzled rows (lds_off)
+  __bf16 v[kTile * D];
 };
 
+// dQ for one (b, query head, 128-query tile).  Per wave 32 queries; S^T and
+// dP^T put the query in the lane, dS^T feeds dQ^T += K^T dS^T as B operand.
 template <int D>
-__global__ __launch_bounds__(kThreads, 1) void bwd_dq_kernel(BwdParams p) {
-  constexpr int PITCH = DqSmem<D>::kPitch;
+__global__ __launch_bounds__(kThreads, 2) void bwd_dq_kernel(BwdParams p) {
   constexpr int KS = D / 16;
   constexpr int DT = D / 32;
   __shared__ DqSmem<D> sm;
 
-  const int qt = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int h = blockIdx.x, b = blockIdx.z;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int g = lane >> 5, n = lane & 31;
   const int hk = h / (p.Hq / p.Hkv);
   const int mb = p.m.Bm > 1 ? b : 0;
-  const int T = p.T, nt = p.nt, words = p.m.words;
+  const int T = p.T, nt = p.m.nt;
+  const int qt = uniform(p.m.row_order[(size_t)mb * nt + blockIdx.y]);
   const int q0 = qt * kTile;
-  const int qrow = q0 + 32 * wave + n;
+  const int qloc = 32 * wave + n;
+  const int qrow = q0 + qloc;
   const bool qvalid = qrow < T;
+  const float c = p.scale_log2;
 
   bf16x8 qf[KS], dof[KS];
   {
@@ -278,32 +253,26 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dq_kernel(BwdParams p) {
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
       const bf16x8 a = *reinterpret_cast<const bf16x8*>(qp + 16 * s + 8 * g);
-      const bf16x8 c = *reinterpret_cast<const bf16x8*>(dp + 16 * s + 8 * g);
+      const bf16x8 cc = *reinterpret_cast<const bf16x8*>(dp + 16 * s + 8 * g);
       qf[s] = qvalid ? a : bf16x8{};
-      dof[s] = qvalid ? c : bf16x8{};
+      dof[s] = qvalid ? cc : bf16x8{};
     }
   }
-  float lse2 = INFINITY, delta = 0.f;
+  float neg_lse = -INFINITY, delta = 0.f;
   if (qvalid) {
     const float l = p.lse2[((size_t)b * p.Hq + h) * T + qrow];
-    lse2 = (l == -INFINITY) ? INFINITY : l;
+    neg_lse = (l == -INFINITY) ? -INFINITY : -l;  // fully masked row: P = 0
     delta = p.delta[((size_t)b * p.Hq + h) * T + qrow];
   }
-  const int32_t* mdoc = p.m.doc + (size_t)mb * T;
-  const uint64_t* mqb = p.m.qbits + (size_t)mb * words * T;
-  const uint64_t* mkb = p.m.kvbits + (size_t)mb * words * T;
-  const int32_t qdoc = qvalid ? mdoc[qrow] : 0;
-  uint64_t qbits[kMaxWords];
-#pragma unroll
-  for (int w = 0; w < kMaxWords; ++w) qbits[w] = (w < words && qvalid) ? mqb[(size_t)w * T + qrow] : 0ull;
 
-  const __bf16* kbase = p.k + b * p.k_sb + hk * p.k_sh;
-  const __bf16* vbase = p.v + b * p.v_sb + hk * p.v_sh;
+  const auto krs = slice_rsrc(p.k + b * p.k_sb + hk * p.k_sh, p.k_st, T, D);
+  const auto vrs = slice_rsrc(p.v + b * p.v_sb + hk * p.v_sh, p.v_st, T, D);
   const size_t row = (size_t)mb * nt + qt;
-  const int npart = p.m.kv_num[row];
-  const int nfull = p.m.full_kv_num[row];
+  const int npart = uniform(p.m.kv_num[row]);
+  const int nfull = uniform(p.m.full_kv_num[row]);
   const int32_t* pidx = p.m.kv_idx + row * nt;
   const int32_t* fidx = p.m.full_kv_idx + row * nt;
+  const uint32_t* bits_base = p.m.tile_bits + (size_t)p.m.kv_bits_off[row] * kTileBitsWords + qloc * 4;
 
   f32x16 dqacc[DT];
 #pragma unroll
@@ -311,42 +280,38 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dq_kernel(BwdParams p) {
 
   for (int it = 0; it < npart + nfull; ++it) {
     const bool partial = it < npart;
-    const int kt = partial ? pidx[it] : fidx[it - npart];
+    const int kt = uniform(partial ? pidx[it] : fidx[it - npart]);
     const int k0 = kt * kTile;
+    uint4 mbits = make_uint4(~0u, ~0u, ~0u, ~0u);
+    if (partial) mbits = *reinterpret_cast<const uint4*>(bits_base + (size_t)it * kTileBitsWords);
     __syncthreads();
-    load_tile<D, PITCH>(sm.k, kbase, p.k_st, k0, T, tid);
-    load_tile<D, PITCH>(sm.v, vbase, p.v_st, k0, T, tid);
-    if (partial && tid < kTile) {
-      const int t = k0 + tid;
-      sm.kdoc[tid] = t < T ? mdoc[t] : 0;
-      for (int w = 0; w < words; ++w) sm.kbits[w][tid] = t < T ? mkb[(size_t)w * T + t] : 0ull;
-    }
+    load_tile_lds<D>(sm.k, krs, p.k_st, k0, tid);
+    load_tile_lds<D>(sm.v, vrs, p.v_st, k0, tid);
     __syncthreads();
+    const uint32_t w4[4] = {mbits.x, mbits.y, mbits.z, mbits.w};
 
-#pragma unroll 1
-    for (int j = 0; j < 4; ++j) {
-      f32x16 sacc = f32x16{}, dpacc = f32x16{};
 #pragma unroll
-      for (int s = 0; s < KS; ++s) {
-        const bf16x8 ka = lds_row8(&sm.k[(32 * j + n) * PITCH + 16 * s + 8 * g]);
-        const bf16x8 va = lds_row8(&sm.v[(32 * j + n) * PITCH + 16 * s + 8 * g]);
+    for (int j = 0; j < 4; ++j) {
+      if (__ballot(w4[j] != 0u) == 0ull) continue;
+      const bool mixed = __ballot(w4[j] != ~0u) != 0ull;
+      f32x16 sacc, dpacc;
+      {
+        const bf16x8 ka = lds_row8<D>(sm.k, 32 * j + n, 8 * g);
+        const bf16x8 va = lds_row8<D>(sm.v, 32 * j + n, 8 * g);
+        if (mixed) sacc = mfma32(ka, qf[0], mask_bias(w4[j] >> (4 * g)));
+        else sacc = mfma32(ka, qf[0], f32x16{});
+        dpacc = mfma32(va, dof[0], f32x16{});
+      }
+#pragma unroll
+      for (int s = 1; s < KS; ++s) {
+        const bf16x8 ka = lds_row8<D>(sm.k, 32 * j + n, 16 * s + 8 * g);
+        const bf16x8 va = lds_row8<D>(sm.v, 32 * j + n, 16 * s + 8 * g);
         sacc = mfma32(ka, qf[s], sacc);
         dpacc = mfma32(va, dof[s], dpacc);
       }
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        const int kk = 32 * j + acc_row(i, g);
-        const int keyi = k0 + kk;
-        float pv = fast_exp2(sacc[i] * p.scale_log2 - lse2);
-        if (partial) {
-          bool ok = qvalid && keyi < T && keyi <= qrow;
-          if (ok && qdoc != sm.kdoc[kk]) {
-            bool hit = false;
-            for (int w = 0; w < words; ++w) hit |= (qbits[w] & sm.kbits[w][kk]) != 0ull;
-            ok = hit;
-          }
-          if (!ok) pv = 0.f;
-        }
+        const float pv = fast_exp2(fmaf(sacc[i], c, neg_lse));
         dpacc[i] = pv * (dpacc[i] - delta);  // dS^T
       }
       // dQ^T += K^T dS^T (contraction over the 32 keys of block j).
@@ -355,7 +320,7 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dq_kernel(BwdParams p) {
         const bf16x8 sb = pack_half(dpacc, h2);
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) {
-          const bf16x8 ka = lds_col8(sm.k, PITCH, 32 * j + 16 * h2, 8, 32 * dt, lane);
+          const bf16x8 ka = lds_col8<D>(sm.k, 32 * j + 16 * h2, 8, 32 * dt, lane);
           dqacc[dt] = mfma32(ka, sb, dqacc[dt]);
         }
       }
@@ -387,7 +352,6 @@ BwdParams make_bwd_params(const TensorView& q, const TensorView& k, const Tensor
   p.lse2 = lse2;
   p.delta = delta;
   p.B = dims.B; p.Hq = dims.Hq; p.Hkv = dims.Hkv; p.T = dims.T;
-  p.nt = (dims.T + kTile - 1) / kTile;
   p.scale = dims.scale;
   p.scale_log2 = dims.scale * kLog2e;
   p.m = mask;
@@ -403,7 +367,8 @@ hipError_t launch_attn_bwd_phase(int phase, const TensorView& q, const TensorVie
                                  const AttnDims& dims, const MaskTables& mask,
                                  hipStream_t stream) {
   const BwdParams p = make_bwd_params(q, k, v, o, dout, lse2, delta, dq, dk, dv, dims, mask);
-  if (p.nt == 0 || dims.B == 0 || dims.Hq == 0) return hipSuccess;
+  const int nt = (dims.T + kTile - 1) / kTile;
+  if (nt == 0 || dims.B == 0 || dims.Hq == 0) return hipSuccess;
   const bool d64 = dims.D == 64;
   if (phase == kBwdDelta) {
     const int64_t rows = (int64_t)dims.B * dims.Hq * dims.T;
@@ -412,11 +377,11 @@ hipError_t launch_attn_bwd_phase(int phase, const TensorView& q, const TensorVie
     if (d64) hipLaunchKernelGGL(bwd_delta_kernel<64>, grid, dim3(kThreads), 0, stream, p);
     else hipLaunchKernelGGL(bwd_delta_kernel<128>, grid, dim3(kThreads), 0, stream, p);
   } else if (phase == kBwdDkDv) {
-    const dim3 grid(p.nt, dims.Hkv, dims.B);
+    const dim3 grid(dims.Hkv, nt, dims.B);
     if (d64) hipLaunchKernelGGL(bwd_dkdv_kernel<64>, grid, dim3(kThreads), 0, stream, p);
     else hipLaunchKernelGGL(bwd_dkdv_kernel<128>, grid, dim3(kThreads), 0, stream, p);
   } else {
-    const dim3 grid(p.nt, dims.Hq, dims.B);
+    const dim3 grid(dims.Hq, nt, dims.B);
     if (d64) hipLaunchKernelGGL(bwd_dq_kernel<64>, grid, dim3(kThreads), 0, stream, p);
     else hipLaunchKernelGGL(bwd_dq_kernel<128>, grid, dim3(kThreads), 0, stream, p);
   }

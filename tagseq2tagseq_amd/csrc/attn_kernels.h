@@ -11,15 +11,10 @@ struct TensorView {
   int64_t sb, sh, st;
 };
 
-// Per-token mask inputs plus the BlockMask tables produced by the metadata pass.
-// Tables are laid out [Bm][nt] (counts) and [Bm][nt][nt] (indices); Bm is 1
-// (one mask shared by every batch row) or B.
+// BlockMask tables produced by the metadata pass ([Bm][nt] / [Bm][nt][nt]).
 struct MaskTables {
-  const int32_t* doc;       // [Bm][T]
-  const uint64_t* qbits;    // [Bm][words][T]
-  const uint64_t* kvbits;   // [Bm][words][T]
-  int words;
   int Bm;
+  int nt;
   const int32_t* kv_num;
   const int32_t* kv_idx;
   const int32_t* full_kv_num;
@@ -28,6 +23,31 @@ struct MaskTables {
   const int32_t* q_idx;
   const int32_t* full_q_num;
   const int32_t* full_q_idx;
+  const int32_t* row_order;
+  const int32_t* col_order;
+  const int32_t* kv_bits_off;
+  const int32_t* q_bits_slot;
+  const uint32_t* tile_bits;  // [slot][2][128][4]
+};
+
+// Writable view of the same tables for the metadata pass.
+struct MaskOut {
+  int Bm;
+  int nt;
+  int8_t* tile_class;
+  int32_t* kv_num;
+  int32_t* kv_idx;
+  int32_t* full_kv_num;
+  int32_t* full_kv_idx;
+  int32_t* q_num;
+  int32_t* q_idx;
+  int32_t* full_q_num;
+  int32_t* full_q_idx;
+  int32_t* row_order;
+  int32_t* col_order;
+  int32_t* kv_bits_off;
+  int32_t* q_bits_slot;
+  uint32_t* tile_bits;
 };
 
 struct AttnDims {
@@ -35,11 +55,10 @@ struct AttnDims {
   float scale;  // softmax scale applied to Q K^T
 };
 
+constexpr int kTileBitsWords = 2 * kTile * 4;  // uint32 words per tile bitmap slot
+
 hipError_t launch_mask_meta(const int32_t* doc, const uint64_t* qbits, const uint64_t* kvbits,
-                            int Bm, int T, int words, int8_t* tile_class, int32_t* kv_num,
-                            int32_t* kv_idx, int32_t* full_kv_num, int32_t* full_kv_idx,
-                            int32_t* q_num, int32_t* q_idx, int32_t* full_q_num,
-                            int32_t* full_q_idx, hipStream_t stream);
+                            int T, int words, const MaskOut& out, hipStream_t stream);
 
 hipError_t launch_attn_fwd_bf16(const TensorView& q, const TensorView& k, const TensorView& v,
                                 const TensorView& o, float* lse2, const AttnDims& dims,
@@ -47,9 +66,9 @@ hipError_t launch_attn_fwd_bf16(const TensorView& q, const TensorView& k, const 
 
 enum BwdPhase { kBwdDelta = 0, kBwdDkDv = 1, kBwdDq = 2 };
 
-// One backward phase.  Unused views may be empty for a phase that does not
-// read them (delta: o, dout; dkdv: q, k, v, dout, lse2, delta, dk, dv; dq: q,
-// k, v, dout, lse2, delta, dq).
+// One backward phase.  Views a phase does not read may be empty (delta: o,
+// dout; dkdv: q, k, v, dout, lse2, delta, dk, dv; dq: q, k, v, dout, lse2,
+// delta, dq).
 hipError_t launch_attn_bwd_phase(int phase, const TensorView& q, const TensorView& k,
                                  const TensorView& v, const TensorView& o,
                                  const TensorView& dout, const float* lse2, float* delta,

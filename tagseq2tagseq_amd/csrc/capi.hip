@@ -33,33 +33,34 @@ t2t::TensorView as_view(const t2t_tensor* t) {
   return t2t::TensorView{t->data, t->stride_b, t->stride_h, t->stride_t};
 }
 
-int check_mask(const t2t_mask* m, int B, bool need_rows, bool need_cols) {
+int check_mask(const t2t_block_mask* m, int B, int T, bool need_rows, bool need_cols) {
   if (!m) return fail(T2T_EINVAL, "mask is NULL");
-  if (!m->doc) return fail(T2T_EINVAL, "mask.doc is NULL");
-  if (m->words < 0 || m->words > T2T_MAX_WORDS)
-    return fail(T2T_EUNSUPPORTED, "mask.words=%d outside [0, %d]", m->words, T2T_MAX_WORDS);
-  if (m->words > 0 && (!m->q_bits || !m->kv_bits))
-    return fail(T2T_EINVAL, "mask.words=%d but q_bits/kv_bits is NULL", m->words);
   if (!(m->mask_batch == 1 || m->mask_batch == B))
     return fail(T2T_EINVAL, "mask.mask_batch=%d must be 1 or B=%d", m->mask_batch, B);
-  if (need_rows && (!m->kv_num || !m->kv_idx || !m->full_kv_num || !m->full_kv_idx))
-    return fail(T2T_EINVAL, "mask row tables (kv_num/kv_idx/full_kv_*) missing");
-  if (need_cols && (!m->q_num || !m->q_idx || !m->full_q_num || !m->full_q_idx))
-    return fail(T2T_EINVAL, "mask column tables (q_num/q_idx/full_q_*) missing");
+  const int nt = (T + t2t::kTile - 1) / t2t::kTile;
+  if (m->num_tiles != nt)
+    return fail(T2T_EINVAL, "mask.num_tiles=%d but T=%d needs %d", m->num_tiles, T, nt);
+  if (need_rows && (!m->kv_num || !m->kv_idx || !m->full_kv_num || !m->full_kv_idx ||
+                    !m->row_order || !m->kv_bits_off))
+    return fail(T2T_EINVAL, "mask row tables (kv_*, row_order, kv_bits_off) missing");
+  if (need_cols && (!m->q_num || !m->q_idx || !m->full_q_num || !m->full_q_idx ||
+                    !m->col_order || !m->q_bits_slot))
+    return fail(T2T_EINVAL, "mask column tables (q_*, col_order, q_bits_slot) missing");
+  if (!m->tile_bits) return fail(T2T_EINVAL, "mask.tile_bits is NULL");
   return T2T_OK;
 }
 
-t2t::MaskTables as_tables(const t2t_mask* m) {
+t2t::MaskTables as_tables(const t2t_block_mask* m) {
   t2t::MaskTables t;
-  t.doc = m->doc;
-  t.qbits = m->q_bits;
-  t.kvbits = m->kv_bits;
-  t.words = m->words;
   t.Bm = m->mask_batch;
+  t.nt = m->num_tiles;
   t.kv_num = m->kv_num; t.kv_idx = m->kv_idx;
   t.full_kv_num = m->full_kv_num; t.full_kv_idx = m->full_kv_idx;
   t.q_num = m->q_num; t.q_idx = m->q_idx;
   t.full_q_num = m->full_q_num; t.full_q_idx = m->full_q_idx;
+  t.row_order = m->row_order; t.col_order = m->col_order;
+  t.kv_bits_off = m->kv_bits_off; t.q_bits_slot = m->q_bits_slot;
+  t.tile_bits = m->tile_bits;
   return t;
 }
 
@@ -82,26 +83,42 @@ const char* t2t_last_error(void) { return g_err; }
 
 int t2t_mask_meta(const int32_t* doc, const uint64_t* q_bits, const uint64_t* kv_bits,
                   int32_t mask_batch, int32_t T, int32_t words, int8_t* tile_class,
-                  int32_t* kv_num, int32_t* kv_idx, int32_t* full_kv_num,
-                  int32_t* full_kv_idx, int32_t* q_num, int32_t* q_idx,
-                  int32_t* full_q_num, int32_t* full_q_idx, void* stream) {
+                  const t2t_block_mask* out, void* stream) {
   if (T < 0 || mask_batch < 0) return fail(T2T_EINVAL, "negative T or mask_batch");
   if (words < 0 || words > T2T_MAX_WORDS)
     return fail(T2T_EUNSUPPORTED, "words=%d outside [0, %d]", words, T2T_MAX_WORDS);
   if (T == 0 || mask_batch == 0) return T2T_OK;
-  if (!doc || (words > 0 && (!q_bits || !kv_bits)) || !tile_class || !kv_num || !kv_idx ||
-      !full_kv_num || !full_kv_idx || !q_num || !q_idx || !full_q_num || !full_q_idx)
+  if (!out) return fail(T2T_EINVAL, "out is NULL");
+  const int nt = (T + t2t::kTile - 1) / t2t::kTile;
+  if (out->mask_batch != mask_batch || out->num_tiles != nt)
+    return fail(T2T_EINVAL, "out describes Bm=%d nt=%d, expected Bm=%d nt=%d", out->mask_batch,
+                out->num_tiles, mask_batch, nt);
+  const int64_t need = (int64_t)mask_batch * nt * (nt + 1) / 2;
+  if (out->tile_bits_slots < need)
+    return fail(T2T_EINVAL, "tile_bits holds %lld slots, %lld needed",
+                (long long)out->tile_bits_slots, (long long)need);
+  if (!doc || (words > 0 && (!q_bits || !kv_bits)) || !tile_class || !out->kv_num ||
+      !out->kv_idx || !out->full_kv_num || !out->full_kv_idx || !out->q_num || !out->q_idx ||
+      !out->full_q_num || !out->full_q_idx || !out->row_order || !out->col_order ||
+      !out->kv_bits_off || !out->q_bits_slot || !out->tile_bits)
     return fail(T2T_EINVAL, "NULL pointer argument");
-  return hip_status(t2t::launch_mask_meta(doc, q_bits, kv_bits, mask_batch, T, words,
-                                          tile_class, kv_num, kv_idx, full_kv_num, full_kv_idx,
-                                          q_num, q_idx, full_q_num, full_q_idx,
+  t2t::MaskOut o;
+  o.Bm = mask_batch; o.nt = nt; o.tile_class = tile_class;
+  o.kv_num = out->kv_num; o.kv_idx = out->kv_idx;
+  o.full_kv_num = out->full_kv_num; o.full_kv_idx = out->full_kv_idx;
+  o.q_num = out->q_num; o.q_idx = out->q_idx;
+  o.full_q_num = out->full_q_num; o.full_q_idx = out->full_q_idx;
+  o.row_order = out->row_order; o.col_order = out->col_order;
+  o.kv_bits_off = out->kv_bits_off; o.q_bits_slot = out->q_bits_slot;
+  o.tile_bits = out->tile_bits;
+  return hip_status(t2t::launch_mask_meta(doc, q_bits, kv_bits, T, words, o,
                                           static_cast<hipStream_t>(stream)),
                     "t2t_mask_meta launch");
 }
 
 int t2t_attn_fwd(const t2t_tensor* q, const t2t_tensor* k, const t2t_tensor* v,
                  const t2t_tensor* o, float* lse2, int32_t B, int32_t Hq, int32_t Hkv,
-                 int32_t T, int32_t D, int32_t dtype, float scale, const t2t_mask* mask,
+                 int32_t T, int32_t D, int32_t dtype, float scale, const t2t_block_mask* mask,
                  void* stream) {
   int rc = check_dims(B, Hq, Hkv, T, D, dtype);
   if (rc) return rc;
@@ -109,7 +126,7 @@ int t2t_attn_fwd(const t2t_tensor* q, const t2t_tensor* k, const t2t_tensor* v,
   if (!view_ok(q) || !view_ok(k) || !view_ok(v) || !view_ok(o))
     return fail(T2T_EINVAL, "q/k/v/o view invalid (NULL, misaligned or bad stride)");
   if (!lse2) return fail(T2T_EINVAL, "lse2 is NULL");
-  rc = check_mask(mask, B, true, false);
+  rc = check_mask(mask, B, T, true, false);
   if (rc) return rc;
   t2t::AttnDims dims{B, Hq, Hkv, T, D, scale};
   return hip_status(t2t::launch_attn_fwd_bf16(as_view(q), as_view(k), as_view(v), as_view(o),
@@ -139,7 +156,7 @@ int t2t_attn_bwd_dkdv(const t2t_tensor* q, const t2t_tensor* k, const t2t_tensor
                       const t2t_tensor* dout, const float* lse2, const float* delta,
                       const t2t_tensor* dk, const t2t_tensor* dv, int32_t B, int32_t Hq,
                       int32_t Hkv, int32_t T, int32_t D, int32_t dtype, float scale,
-                      const t2t_mask* mask, void* stream) {
+                      const t2t_block_mask* mask, void* stream) {
   int rc = check_dims(B, Hq, Hkv, T, D, dtype);
   if (rc) return rc;
   if (B == 0 || Hq == 0 || T == 0) return T2T_OK;
@@ -147,7 +164,7 @@ int t2t_attn_bwd_dkdv(const t2t_tensor* q, const t2t_tensor* k, const t2t_tensor
       !view_ok(dv))
     return fail(T2T_EINVAL, "tensor view invalid (NULL, misaligned or bad stride)");
   if (!lse2 || !delta) return fail(T2T_EINVAL, "lse2/delta is NULL");
-  rc = check_mask(mask, B, false, true);
+  rc = check_mask(mask, B, T, false, true);
   if (rc) return rc;
   const t2t::TensorView none{nullptr, 0, 0, 0};
   t2t::AttnDims dims{B, Hq, Hkv, T, D, scale};
@@ -162,14 +179,14 @@ int t2t_attn_bwd_dkdv(const t2t_tensor* q, const t2t_tensor* k, const t2t_tensor
 int t2t_attn_bwd_dq(const t2t_tensor* q, const t2t_tensor* k, const t2t_tensor* v,
                     const t2t_tensor* dout, const float* lse2, const float* delta,
                     const t2t_tensor* dq, int32_t B, int32_t Hq, int32_t Hkv, int32_t T,
-                    int32_t D, int32_t dtype, float scale, const t2t_mask* mask, void* stream) {
+                    int32_t D, int32_t dtype, float scale, const t2t_block_mask* mask, void* stream) {
   int rc = check_dims(B, Hq, Hkv, T, D, dtype);
   if (rc) return rc;
   if (B == 0 || Hq == 0 || T == 0) return T2T_OK;
   if (!view_ok(q) || !view_ok(k) || !view_ok(v) || !view_ok(dout) || !view_ok(dq))
     return fail(T2T_EINVAL, "tensor view invalid (NULL, misaligned or bad stride)");
   if (!lse2 || !delta) return fail(T2T_EINVAL, "lse2/delta is NULL");
-  rc = check_mask(mask, B, true, false);
+  rc = check_mask(mask, B, T, true, false);
   if (rc) return rc;
   const t2t::TensorView none{nullptr, 0, 0, 0};
   t2t::AttnDims dims{B, Hq, Hkv, T, D, scale};
@@ -185,7 +202,7 @@ int t2t_attn_bwd(const t2t_tensor* q, const t2t_tensor* k, const t2t_tensor* v,
                  const t2t_tensor* o, const t2t_tensor* dout, const float* lse2,
                  float* delta, const t2t_tensor* dq, const t2t_tensor* dk,
                  const t2t_tensor* dv, int32_t B, int32_t Hq, int32_t Hkv, int32_t T,
-                 int32_t D, int32_t dtype, float scale, const t2t_mask* mask, void* stream) {
+                 int32_t D, int32_t dtype, float scale, const t2t_block_mask* mask, void* stream) {
   int rc = check_dims(B, Hq, Hkv, T, D, dtype);
   if (rc) return rc;
   if (B == 0 || Hq == 0 || T == 0) return T2T_OK;

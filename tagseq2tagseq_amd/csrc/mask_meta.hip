@@ -1,6 +1,6 @@
 // Mask-metadata pass: per-token document ids and grant words -> 128 x 128 tile
-// classification (skip / partial / full) and the ordered index lists of a
-// BlockMask.
+// classification (skip / partial / full), the ordered index lists of a
+// BlockMask, launch orders and per-partial-tile allowed-pair bitmaps.
 //
 // Semantics restated from
 //   * mask_mod:  model/graph_traversal/cross_doc_mask.py:348-357
@@ -20,7 +20,10 @@
 // one predicate evaluation per run pair plus the causal geometry of the
 // rectangle.  Packed documents give 1-3 runs per 128 tokens, so a tile costs a
 // handful of evaluations instead of 16384.
-#include "t2t_common.h"
+//
+// Launches: (1) classify every tile, (2) row and column lists, (3) bitmap
+// slot offsets and launch orders, (4) partial-tile bitmaps.
+#include "attn_kernels.h"
 
 namespace t2t {
 
@@ -124,107 +127,251 @@ __device__ void wave_ordered(const int8_t* cls, int stride, int n, int8_t want,
 
 }  // namespace
 
-// grid (nt, Bm); block 256; dynamic LDS: nt bytes of row classes.
-__global__ __launch_bounds__(kThreads) void mask_classify_rows(
+// (1) grid (nt, nt, Bm); block 64: one wave decides one tile (kt = x, qt = y).
+__global__ __launch_bounds__(64) void mask_classify_tiles(
     const int32_t* __restrict__ doc_all, const uint64_t* __restrict__ qbits_all,
-    const uint64_t* __restrict__ kvbits_all, int T, int words, int nt,
-    int8_t* __restrict__ tile_class, int32_t* __restrict__ kv_num,
-    int32_t* __restrict__ kv_idx, int32_t* __restrict__ full_kv_num,
-    int32_t* __restrict__ full_kv_idx) {
-  extern __shared__ int8_t row_cls[];
+    const uint64_t* __restrict__ kvbits_all, int T, int words, MaskOut out) {
   __shared__ int q_starts[kTile + 1];
-  __shared__ int kv_starts[kWaves][kTile + 1];
-  __shared__ int n_qruns;
-
-  const int qt = blockIdx.x;
-  const int b = blockIdx.y;
-  const int wave = threadIdx.x >> 6;
-  const int lane = threadIdx.x & 63;
+  __shared__ int kv_starts[kTile + 1];
+  const int nt = out.nt;
+  const int kt = blockIdx.x, qt = blockIdx.y, b = blockIdx.z;
+  const int lane = threadIdx.x;
+  int8_t* dst = out.tile_class + ((size_t)b * nt + qt) * nt + kt;
+  if (kt > qt) {  // every pair has kv > q
+    if (lane == 0) *dst = kSkip;
+    return;
+  }
   const int32_t* doc = doc_all + (size_t)b * T;
   const uint64_t* qbits = qbits_all + (size_t)b * words * T;
   const uint64_t* kvbits = kvbits_all + (size_t)b * words * T;
-  const int q0 = qt * kTile;
-  const int qvalid = min(kTile, T - q0);
-
-  if (wave == 0) {
-    const int n = wave_runs(doc, qbits, words, T, q0, q_starts);
-    if (lane == 0) n_qruns = n;
-  }
+  const int q0 = qt * kTile, k0 = kt * kTile;
+  const int qvalid = min(kTile, T - q0), kvalid = min(kTile, T - k0);
+  const int nqr = wave_runs(doc, qbits, words, T, q0, q_starts);
+  const int nkr = wave_runs(doc, kvbits, words, T, k0, kv_starts);
   __syncthreads();
-  const int nqr = n_qruns;
-
-  for (int kt = wave; kt < nt; kt += kWaves) {
-    int8_t cls = kSkip;
-    if (kt <= qt) {
-      const int k0 = kt * kTile;
-      const int kvalid = min(kTile, T - k0);
-      const int nkr = wave_runs(doc, kvbits, words, T, k0, kv_starts[wave]);
-      // Padding rows/columns are False pairs: such a tile can never be full.
-      bool any_true = false;
-      bool any_false = (qvalid < kTile) || (kvalid < kTile);
-      const int npairs = nqr * nkr;
-      for (int p0 = 0; p0 < npairs; p0 += 64) {
-        const int p = p0 + lane;
-        bool t = false, f = false;
-        if (p < npairs) {
-          const int r = p / nkr, s = p - r * nkr;
-          const int qa = q0 + q_starts[r], qb = q0 + q_starts[r + 1];
-          const int ka = k0 + kv_starts[wave][s], kb = k0 + kv_starts[wave][s + 1];
-          const bool v = sig_pair_allowed(doc, qbits, kvbits, words, T, qa, ka);
-          const bool exists_ge = (qb - 1) >= ka;   // some pair with q >= kv
-          const bool exists_lt = qa < (kb - 1);    // some pair with q < kv
-          t = v && exists_ge;
-          f = !v || exists_lt;
-        }
-        any_true = any_true || (__ballot(t) != 0);
-        any_false = any_false || (__ballot(f) != 0);
-        if (any_true && any_false) break;
-      }
-      cls = any_true ? (any_false ? kPartial : kFull) : kSkip;
+  // Padding rows/columns are False pairs: such a tile can never be full.
+  bool any_true = false;
+  bool any_false = (qvalid < kTile) || (kvalid < kTile);
+  const int npairs = nqr * nkr;
+  for (int p0 = 0; p0 < npairs; p0 += 64) {
+    const int p = p0 + lane;
+    bool t = false, f = false;
+    if (p < npairs) {
+      const int r = p / nkr, s = p - r * nkr;
+      const int qa = q0 + q_starts[r], qb = q0 + q_starts[r + 1];
+      const int ka = k0 + kv_starts[s], kb = k0 + kv_starts[s + 1];
+      const bool v = sig_pair_allowed(doc, qbits, kvbits, words, T, qa, ka);
+      const bool exists_ge = (qb - 1) >= ka;   // some pair with q >= kv
+      const bool exists_lt = qa < (kb - 1);    // some pair with q < kv
+      t = v && exists_ge;
+      f = !v || exists_lt;
     }
-    if (lane == 0) row_cls[kt] = cls;
+    any_true = any_true || (__ballot(t) != 0);
+    any_false = any_false || (__ballot(f) != 0);
+    if (any_true && any_false) break;
   }
-  __syncthreads();
+  if (lane == 0) *dst = any_true ? (any_false ? kPartial : kFull) : kSkip;
+}
 
-  int8_t* out_row = tile_class + ((size_t)b * nt + qt) * nt;
-  for (int i = threadIdx.x; i < nt; i += kThreads) out_row[i] = row_cls[i];
-  const size_t row = (size_t)b * nt + qt;
-  if (wave == 0) {
-    wave_ordered(row_cls, 1, nt, kPartial, kv_num + row, kv_idx + row * nt);
-  } else if (wave == 1) {
-    wave_ordered(row_cls, 1, nt, kFull, full_kv_num + row, full_kv_idx + row * nt);
+// (2) grid (nt, Bm); block 256.  Wave 0/1: partial / full list of row x;
+// wave 2/3: partial / full list of column x.
+__global__ __launch_bounds__(kThreads) void mask_lists(MaskOut out) {
+  const int nt = out.nt;
+  const int i = blockIdx.x, b = blockIdx.y;
+  const int wave = threadIdx.x >> 6;
+  const int8_t* grid = out.tile_class + (size_t)b * nt * nt;
+  const size_t r = (size_t)b * nt + i;
+  if (wave == 0)
+    wave_ordered(grid + (size_t)i * nt, 1, nt, kPartial, out.kv_num + r, out.kv_idx + r * nt);
+  else if (wave == 1)
+    wave_ordered(grid + (size_t)i * nt, 1, nt, kFull, out.full_kv_num + r, out.full_kv_idx + r * nt);
+  else if (wave == 2)
+    wave_ordered(grid + i, nt, nt, kPartial, out.q_num + r, out.q_idx + r * nt);
+  else
+    wave_ordered(grid + i, nt, nt, kFull, out.full_q_num + r, out.full_q_idx + r * nt);
+}
+
+// (3) grid (1); block 256.  kv_bits_off = exclusive prefix sum of kv_num over
+// (b, row); row / column launch orders ranked by descending non-skip tile
+// count (ties: higher index first).
+__global__ __launch_bounds__(kThreads) void mask_offsets_schedule(MaskOut out) {
+  __shared__ int scan[kThreads];
+  const int nt = out.nt;
+  const int tid = threadIdx.x;
+  const int n = out.Bm * nt;
+  int carry = 0;
+  for (int c = 0; c < n; c += kThreads) {
+    const int i = c + tid;
+    const int v = i < n ? out.kv_num[i] : 0;
+    scan[tid] = v;
+    __syncthreads();
+    for (int off = 1; off < kThreads; off <<= 1) {
+      const int add = tid >= off ? scan[tid - off] : 0;
+      __syncthreads();
+      scan[tid] += add;
+      __syncthreads();
+    }
+    if (i < n) out.kv_bits_off[i] = carry + scan[tid] - v;
+    carry += scan[kThreads - 1];
+    __syncthreads();
+  }
+  for (int b = 0; b < out.Bm; ++b) {
+    const int32_t* rn = out.kv_num + (size_t)b * nt;
+    const int32_t* rf = out.full_kv_num + (size_t)b * nt;
+    const int32_t* cn = out.q_num + (size_t)b * nt;
+    const int32_t* cf = out.full_q_num + (size_t)b * nt;
+    for (int i = tid; i < nt; i += kThreads) {
+      const int ri = rn[i] + rf[i], ci = cn[i] + cf[i];
+      int rr = 0, rc = 0;
+      for (int j = 0; j < nt; ++j) {
+        const int rj = rn[j] + rf[j], cj = cn[j] + cf[j];
+        rr += (rj > ri) || (rj == ri && j > i);
+        rc += (cj > ci) || (cj == ci && j > i);
+      }
+      out.row_order[(size_t)b * nt + rr] = i;
+      out.col_order[(size_t)b * nt + rc] = i;
+    }
   }
 }
 
-// grid (nt, Bm); block 128 (wave 0: partial list, wave 1: full list).
-__global__ __launch_bounds__(128) void mask_columns(
-    const int8_t* __restrict__ tile_class, int nt, int32_t* __restrict__ q_num,
-    int32_t* __restrict__ q_idx, int32_t* __restrict__ full_q_num,
-    int32_t* __restrict__ full_q_idx) {
-  const int kt = blockIdx.x;
-  const int b = blockIdx.y;
-  const int wave = threadIdx.x >> 6;
-  const int8_t* col = tile_class + (size_t)b * nt * nt + kt;
-  const size_t row = (size_t)b * nt + kt;
-  if (wave == 0)
-    wave_ordered(col, nt, nt, kPartial, q_num + row, q_idx + row * nt);
-  else
-    wave_ordered(col, nt, nt, kFull, full_q_num + row, full_q_idx + row * nt);
+namespace {
+
+// Set bits [lo, hi) of a 128-bit mask held as four 32-bit words.
+__device__ __forceinline__ void set_bit_range(uint32_t acc[4], int lo, int hi) {
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const int a = max(lo - 32 * w, 0), z = min(hi - 32 * w, 32);
+    if (a < z) {
+      const uint32_t upto = z == 32 ? ~0u : ((1u << z) - 1u);
+      acc[w] |= upto & ~((1u << a) - 1u);
+    }
+  }
+}
+
+__device__ __forceinline__ bool lds_pair_allowed(int32_t da, int32_t db, const uint64_t* ba,
+                                                 const uint64_t* bb, int stride_a, int stride_b,
+                                                 int words) {
+  if (da == db) return true;
+  for (int w = 0; w < words; ++w)
+    if (ba[w * stride_a] & bb[w * stride_b]) return true;
+  return false;
+}
+
+}  // namespace
+
+// (4) grid (nt, nt, Bm); block 256.  For a partial tile (kt = x, qt = y): its
+// slot (row-major numbering over (b, qt, list position)), both bitmap
+// orientations, and its entry in the column's slot list.  A row of the
+// bitmap is built run by run: within a run of keys with one signature the
+// non-causal predicate is constant, so one evaluation sets a whole bit range;
+// the causal and padding limits are applied last.
+__global__ __launch_bounds__(kThreads) void mask_tile_bits(
+    const int32_t* __restrict__ doc_all, const uint64_t* __restrict__ qbits_all,
+    const uint64_t* __restrict__ kvbits_all, int T, int words, MaskOut out) {
+  __shared__ int32_t qdoc[kTile], kdoc[kTile];
+  __shared__ uint64_t qb[kMaxWords][kTile], kb[kMaxWords][kTile];
+  __shared__ int q_starts[kTile + 1], kv_starts[kTile + 1];
+  __shared__ int n_qr, n_kr, pos_row, pos_col;
+  const int nt = out.nt;
+  const int kt = blockIdx.x, qt = blockIdx.y, b = blockIdx.z;
+  if (kt > qt) return;
+  const int8_t* grid = out.tile_class + (size_t)b * nt * nt;
+  if (grid[(size_t)qt * nt + kt] != kPartial) return;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int32_t* doc = doc_all + (size_t)b * T;
+  const uint64_t* qbits = qbits_all + (size_t)b * words * T;
+  const uint64_t* kvbits = kvbits_all + (size_t)b * words * T;
+  const int q0 = qt * kTile, k0 = kt * kTile;
+
+  if (wave == 0) {  // position among the row's partial tiles (columns < kt)
+    int cnt = 0;
+    for (int c = 0; c < kt; c += 64) {
+      const int j = c + lane;
+      cnt += __popcll(__ballot(j < kt && grid[(size_t)qt * nt + j] == kPartial));
+    }
+    if (lane == 0) pos_row = cnt;
+  } else if (wave == 1) {  // position among the column's partial tiles (rows < qt)
+    int cnt = 0;
+    for (int c = 0; c < qt; c += 64) {
+      const int j = c + lane;
+      cnt += __popcll(__ballot(j < qt && grid[(size_t)j * nt + kt] == kPartial));
+    }
+    if (lane == 0) pos_col = cnt;
+  } else if (wave == 2) {
+    const int n = wave_runs(doc, qbits, words, T, q0, q_starts);
+    if (lane == 0) n_qr = n;
+  } else {
+    const int n = wave_runs(doc, kvbits, words, T, k0, kv_starts);
+    if (lane == 0) n_kr = n;
+  }
+  if (tid < kTile) {
+    const int t = q0 + tid;
+    qdoc[tid] = t < T ? doc[t] : 0;
+    for (int w = 0; w < words; ++w) qb[w][tid] = t < T ? qbits[(size_t)w * T + t] : 0ull;
+  } else {
+    const int c = tid - kTile, t = k0 + c;
+    kdoc[c] = t < T ? doc[t] : 0;
+    for (int w = 0; w < words; ++w) kb[w][c] = t < T ? kvbits[(size_t)w * T + t] : 0ull;
+  }
+  __syncthreads();
+  const int slot = out.kv_bits_off[(size_t)b * nt + qt] + pos_row;
+  uint32_t acc[4] = {0u, 0u, 0u, 0u};
+  if (tid < kTile) {
+    // row orientation: query q0 + tid against the tile's keys
+    const int r = tid, q = q0 + r;
+    if (q < T) {
+      for (int s = 0; s < n_kr; ++s) {
+        const int a = kv_starts[s], z = kv_starts[s + 1];
+        if (lds_pair_allowed(qdoc[r], kdoc[a], &qb[0][r], &kb[0][a], kTile, kTile, words))
+          set_bit_range(acc, a, z);
+      }
+      // causal: keys k0 + kk <= q; padding keys (>= T) are outside every run
+      const int lim = q - k0 + 1;  // allowed kk < lim
+      uint32_t cm[4] = {0u, 0u, 0u, 0u};
+      set_bit_range(cm, 0, min(max(lim, 0), kTile));
+#pragma unroll
+      for (int w = 0; w < 4; ++w) acc[w] &= cm[w];
+    }
+  } else {
+    // column orientation: key k0 + c against the tile's queries
+    const int c = tid - kTile, key = k0 + c;
+    if (key < T) {
+      for (int s = 0; s < n_qr; ++s) {
+        const int a = q_starts[s], z = q_starts[s + 1];
+        if (lds_pair_allowed(qdoc[a], kdoc[c], &qb[0][a], &kb[0][c], kTile, kTile, words))
+          set_bit_range(acc, a, z);
+      }
+      // causal: queries q0 + qq >= key
+      const int from = key - q0;  // allowed qq >= from
+      uint32_t cm[4] = {0u, 0u, 0u, 0u};
+      set_bit_range(cm, min(max(from, 0), kTile), kTile);
+#pragma unroll
+      for (int w = 0; w < 4; ++w) acc[w] &= cm[w];
+    }
+  }
+  uint32_t* dst = out.tile_bits + (size_t)slot * kTileBitsWords +
+                  (tid < kTile ? tid * 4 : kTile * 4 + (tid - kTile) * 4);
+  *reinterpret_cast<uint4*>(dst) = make_uint4(acc[0], acc[1], acc[2], acc[3]);
+  if (tid == 0) out.q_bits_slot[((size_t)b * nt + kt) * nt + pos_col] = slot;
 }
 
 hipError_t launch_mask_meta(const int32_t* doc, const uint64_t* qbits, const uint64_t* kvbits,
-                            int Bm, int T, int words, int8_t* tile_class, int32_t* kv_num,
-                            int32_t* kv_idx, int32_t* full_kv_num, int32_t* full_kv_idx,
-                            int32_t* q_num, int32_t* q_idx, int32_t* full_q_num,
-                            int32_t* full_q_idx, hipStream_t stream) {
-  const int nt = (T + kTile - 1) / kTile;
-  if (nt == 0 || Bm == 0) return hipSuccess;
-  hipLaunchKernelGGL(mask_classify_rows, dim3(nt, Bm), dim3(kThreads), nt, stream, doc, qbits,
-                     kvbits, T, words, nt, tile_class, kv_num, kv_idx, full_kv_num, full_kv_idx);
+                            int T, int words, const MaskOut& out, hipStream_t stream) {
+  const int nt = out.nt;
+  if (nt == 0 || out.Bm == 0) return hipSuccess;
+  const dim3 tiles(nt, nt, out.Bm);
+  hipLaunchKernelGGL(mask_classify_tiles, tiles, dim3(64), 0, stream, doc, qbits, kvbits, T,
+                     words, out);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(mask_columns, dim3(nt, Bm), dim3(128), 0, stream, tile_class, nt, q_num,
-                     q_idx, full_q_num, full_q_idx);
+  hipLaunchKernelGGL(mask_lists, dim3(nt, out.Bm), dim3(kThreads), 0, stream, out);
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(mask_offsets_schedule, dim3(1), dim3(kThreads), 0, stream, out);
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(mask_tile_bits, tiles, dim3(kThreads), 0, stream, doc, qbits, kvbits, T,
+                     words, out);
   return hipGetLastError();
 }
 

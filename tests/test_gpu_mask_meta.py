@@ -16,6 +16,55 @@ TABLES = ["kv_num_blocks", "kv_indices", "full_kv_num_blocks", "full_kv_indices"
           "q_num_blocks", "q_indices", "full_q_num_blocks", "full_q_indices"]
 
 
+def _pack_bits(tile: np.ndarray) -> np.ndarray:
+    """bool [128, 128] -> uint32 [128, 4], bit j of word w = tile[r, 32 w + j]."""
+    return np.packbits(tile, axis=1, bitorder="little").view("<u4").reshape(128, 4)
+
+
+def _check_extras(bm, b, doc, qb, kb, label):
+    """Launch orders, bitmap slots and partial-tile bitmaps against the oracle."""
+    T = doc.shape[0]
+    nt = (T + 127) // 128
+    kv_num = bm.kv_num_blocks[b, 0].cpu().numpy()
+    full_num = bm.full_kv_num_blocks[b, 0].cpu().numpy()
+    kv_idx = bm.kv_indices[b, 0].cpu().numpy()
+    q_num = bm.q_num_blocks[b, 0].cpu().numpy()
+    q_full = bm.full_q_num_blocks[b, 0].cpu().numpy()
+    q_idx = bm.q_indices[b, 0].cpu().numpy()
+    row_order = bm.row_order[b].cpu().numpy()
+    col_order = bm.col_order[b].cpu().numpy()
+    off = bm.kv_bits_off[b].cpu().numpy()
+    slot_col = bm.q_bits_slot[b].cpu().numpy()
+    bits = bm.tile_bits.cpu().numpy()
+    assert sorted(row_order.tolist()) == list(range(nt)), f"{label}: row_order not a permutation"
+    assert sorted(col_order.tolist()) == list(range(nt)), f"{label}: col_order not a permutation"
+    rc = (kv_num + full_num)[row_order]
+    cc = (q_num + q_full)[col_order]
+    assert (np.diff(rc) <= 0).all() and (np.diff(cc) <= 0).all(), f"{label}: orders not longest-first"
+    base = int(bm.kv_num_blocks[:b].sum().item())
+    exp_off = base + np.concatenate([[0], np.cumsum(kv_num)[:-1]])
+    np.testing.assert_array_equal(off, exp_off, err_msg=f"{label}: kv_bits_off")
+    row_slot = {}
+    pad = nt * 128 - T
+    for qt in range(nt):
+        if kv_num[qt] == 0:
+            continue
+        rows = mo.dense_mask(doc, qb, kb, (qt * 128, min(T, qt * 128 + 128)))
+        rows = np.pad(rows, ((0, 128 - rows.shape[0]), (0, pad)))
+        for i in range(kv_num[qt]):
+            kt = kv_idx[qt, i]
+            slot = off[qt] + i
+            row_slot[(qt, kt)] = slot
+            tile = rows[:, kt * 128:(kt + 1) * 128]
+            np.testing.assert_array_equal(bits[slot, 0].view("<u4"), _pack_bits(tile),
+                                          err_msg=f"{label}: row bits tile ({qt},{kt})")
+            np.testing.assert_array_equal(bits[slot, 1].view("<u4"), _pack_bits(tile.T.copy()),
+                                          err_msg=f"{label}: column bits tile ({qt},{kt})")
+    for kt in range(nt):
+        for i in range(q_num[kt]):
+            assert slot_col[kt, i] == row_slot[(q_idx[kt, i], kt)], f"{label}: q_bits_slot ({kt},{i})"
+
+
 def _check(bm, rows_np, label):
     tc = bm.tile_class.cpu().numpy()
     got = {name: getattr(bm, name).cpu().numpy() for name in TABLES}
@@ -26,6 +75,7 @@ def _check(bm, rows_np, label):
         np.testing.assert_array_equal(tc[b], exp_cls, err_msg=f"{label} b={b}: tile classes")
         for name in TABLES:
             np.testing.assert_array_equal(got[name][b, 0], ref[name], err_msg=f"{label} b={b}: {name}")
+        _check_extras(bm, b, doc, qb, kb, f"{label} b={b}")
 
 
 def _run(rows_np, device, label):
@@ -82,5 +132,9 @@ def test_deterministic(gpu_device):
     rows = [row_arrays(r) for r in synth.config_rows(3, seed=1, T=4096)]
     a = _run(rows, gpu_device, "det a")
     b = _run(rows, gpu_device, "det b")
-    for name in TABLES + ["tile_class"]:
-        assert torch.equal(getattr(a, name), getattr(b, name))
+    for name in TABLES + ["tile_class", "row_order", "col_order", "kv_bits_off"]:
+        assert torch.equal(getattr(a, name), getattr(b, name)), name
+    # q_bits_slot is defined for the first q_num_blocks entries of each column
+    nt = a.num_tiles
+    valid = torch.arange(nt, device=a.q_num_blocks.device)[None, None, :] < a.q_num_blocks[:, 0, :, None]
+    assert torch.equal(a.q_bits_slot[valid], b.q_bits_slot[valid])
