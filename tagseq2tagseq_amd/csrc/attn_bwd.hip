@@ -77,50 +77,54 @@ __global__ __launch_bounds__(kThreads) void bwd_delta_kernel(BwdParams p) {
   if (rowid < nrows && sub == 0) p.delta[rowid] = acc;
 }
 
+constexpr int kDkdvThreads = 512;  // 8 waves: 4 key groups x 2 query halves
+
 template <int D>
 struct DkdvSmem {
-  __bf16 q[kTile * D];     // swizzled rows (lds_off)
-  __bf16 dout[kTile * D];
-  float lse2[kTile];
-  float delta[kTile];
+  __bf16 k[kTile * pitch<D>()];       // this work-group's keys / values
+  __bf16 v[kTile * pitch<D>()];
+  union {
+    struct {
+      __bf16 q[kTile * pitch<D>()];   // current query tile
+      __bf16 dout[kTile * pitch<D>()];
+      float lse2[kTile];              // per query, in accumulator-row order
+      float delta[kTile];
+    } t;
+    float red[4][D / 32][16][64];  // partial dK or dV of the second query half
+  };
 };
 
-// dK, dV for one (b, kv head, 128-key tile).  Per wave 32 keys; S = Q K^T and
+// dK, dV for one (b, kv head, 128-key tile).  8 waves: wave (kw, qh) owns
+// keys 32 kw .. 32 kw + 31 and queries 64 qh .. 64 qh + 63 of every query
+// tile; the two query halves are summed through LDS at the end.  S = Q K^T and
 // dP = dO V^T put the key in the lane and the query in the accumulator rows,
 // so P and dS feed dV^T += dO^T P and dK^T += Q^T dS directly as B operands.
 template <int D>
-__global__ __launch_bounds__(kThreads, 1) void bwd_dkdv_kernel(BwdParams p) {
+__global__ __launch_bounds__(kDkdvThreads, 1) void bwd_dkdv_kernel(BwdParams p) {
   constexpr int KS = D / 16;
   constexpr int DT = D / 32;
   __shared__ DkdvSmem<D> sm;
 
   const int hk = blockIdx.x, b = blockIdx.z;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int kw = wave & 3, qh = wave >> 2;
   const int g = lane >> 5, n = lane & 31;
   const int G = p.Hq / p.Hkv;
   const int mb = p.m.Bm > 1 ? b : 0;
   const int T = p.T, nt = p.m.nt;
   const int kt = uniform(p.m.col_order[(size_t)mb * nt + blockIdx.y]);
   const int k0 = kt * kTile;
-  const int kloc = 32 * wave + n;
+  const int kloc = 32 * kw + n;
   const int key = k0 + kloc;
   const bool kvalid = key < T;
   const float c = p.scale_log2;
 
-  // K and V as the B operand (k = d, n = key): lane (g, n) holds row `key`.
-  bf16x8 kf[KS], vf[KS];
-  {
-    const int kr = kvalid ? key : 0;
-    const __bf16* kp = p.k + b * p.k_sb + hk * p.k_sh + (int64_t)kr * p.k_st;
-    const __bf16* vp = p.v + b * p.v_sb + hk * p.v_sh + (int64_t)kr * p.v_st;
-#pragma unroll
-    for (int s = 0; s < KS; ++s) {
-      const bf16x8 a = *reinterpret_cast<const bf16x8*>(kp + 16 * s + 8 * g);
-      const bf16x8 cc = *reinterpret_cast<const bf16x8*>(vp + 16 * s + 8 * g);
-      kf[s] = kvalid ? a : bf16x8{};
-      vf[s] = kvalid ? cc : bf16x8{};
-    }
-  }
+  // K and V of the key tile stay in LDS; lane (g, n) reads row kloc as the B
+  // operand (k = d, n = key) of S = Q K^T and dP = dO V^T.
+  load_tile_lds<D, kDkdvThreads>(sm.k, slice_rsrc(p.k + b * p.k_sb + hk * p.k_sh, p.k_st, T, D),
+                                 p.k_st, k0, tid);
+  load_tile_lds<D, kDkdvThreads>(sm.v, slice_rsrc(p.v + b * p.v_sb + hk * p.v_sh, p.v_st, T, D),
+                                 p.v_st, k0, tid);
 
   const size_t col = (size_t)mb * nt + kt;
   const int npart = uniform(p.m.q_num[col]);
@@ -144,51 +148,57 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkdv_kernel(BwdParams p) {
       const bool partial = it < npart;
       const int qt = uniform(partial ? pidx[it] : fidx[it - npart]);
       const int q0 = qt * kTile;
-      uint4 mbits = make_uint4(~0u, ~0u, ~0u, ~0u);
+      uint2 mbits = make_uint2(~0u, ~0u);
       if (partial)
-        mbits = *reinterpret_cast<const uint4*>(bits_col + (size_t)uniform(pslot[it]) * kTileBitsWords);
+        mbits = *reinterpret_cast<const uint2*>(bits_col + (size_t)uniform(pslot[it]) * kTileBitsWords + 2 * qh);
       __syncthreads();
-      load_tile_lds<D>(sm.q, qrs, p.q_st, q0, tid);
-      load_tile_lds<D>(sm.dout, dors, p.do_st, q0, tid);
+      load_tile_lds<D, kDkdvThreads>(sm.t.q, qrs, p.q_st, q0, tid);
+      load_tile_lds<D, kDkdvThreads>(sm.t.dout, dors, p.do_st, q0, tid);
       if (tid < kTile) {
-        const int t = q0 + tid;
+        // slot 32 qs + m holds query 32 qs + tok_perm(m) (accumulator-row order)
+        const int t = q0 + (tid & ~31) + tok_perm(tid & 31);
         const float l = t < T ? lrow[t] : -INFINITY;
         // Fully masked rows (LSE = -inf) carry P = 0: park them at +inf so
         // exp2(s * c - lse) vanishes.
-        sm.lse2[tid] = (l == -INFINITY) ? INFINITY : l;
-        sm.delta[tid] = t < T ? drow[t] : 0.f;
+        sm.t.lse2[tid] = (l == -INFINITY) ? INFINITY : l;
+        sm.t.delta[tid] = t < T ? drow[t] : 0.f;
       }
       __syncthreads();
-      const uint32_t w4[4] = {mbits.x, mbits.y, mbits.z, mbits.w};
+      const uint32_t w2[2] = {mbits.x, mbits.y};
 
 #pragma unroll
-      for (int qs = 0; qs < 4; ++qs) {
+      for (int qq = 0; qq < 2; ++qq) {
+        const int qs = 2 * qh + qq;
         // 32 queries x this wave's 32 keys: empty blocks are skipped, mixed
         // blocks are masked through the accumulator seed (full tiles carry
         // all-ones words).
-        if (__ballot(w4[qs] != 0u) == 0ull) continue;
-        const bool mixed = __ballot(w4[qs] != ~0u) != 0ull;
+        if (__ballot(w2[qq] != 0u) == 0ull) continue;
+        const bool mixed = __ballot(w2[qq] != ~0u) != 0ull;
         f32x16 sacc, dpacc;
         {
-          const bf16x8 qa = lds_row8<D>(sm.q, 32 * qs + n, 8 * g);
-          const bf16x8 da = lds_row8<D>(sm.dout, 32 * qs + n, 8 * g);
-          if (mixed) sacc = mfma32(qa, kf[0], mask_bias(w4[qs] >> (4 * g)));
-          else sacc = mfma32(qa, kf[0], f32x16{});
-          dpacc = mfma32(da, vf[0], f32x16{});
+          const bf16x8 qa = lds_row8<D>(sm.t.q, 32 * qs + tok_perm(n), 8 * g);
+          const bf16x8 da = lds_row8<D>(sm.t.dout, 32 * qs + tok_perm(n), 8 * g);
+          const bf16x8 kb = lds_row8<D>(sm.k, kloc, 8 * g);
+          const bf16x8 vb = lds_row8<D>(sm.v, kloc, 8 * g);
+          if (mixed) sacc = mfma32(qa, kb, mask_bias(w2[qq] >> g));
+          else sacc = mfma32(qa, kb, f32x16{});
+          dpacc = mfma32(da, vb, f32x16{});
         }
 #pragma unroll
         for (int s = 1; s < KS; ++s) {
-          const bf16x8 qa = lds_row8<D>(sm.q, 32 * qs + n, 16 * s + 8 * g);
-          const bf16x8 da = lds_row8<D>(sm.dout, 32 * qs + n, 16 * s + 8 * g);
-          sacc = mfma32(qa, kf[s], sacc);
-          dpacc = mfma32(da, vf[s], dpacc);
+          const bf16x8 qa = lds_row8<D>(sm.t.q, 32 * qs + tok_perm(n), 16 * s + 8 * g);
+          const bf16x8 da = lds_row8<D>(sm.t.dout, 32 * qs + tok_perm(n), 16 * s + 8 * g);
+          const bf16x8 kb = lds_row8<D>(sm.k, kloc, 16 * s + 8 * g);
+          const bf16x8 vb = lds_row8<D>(sm.v, kloc, 16 * s + 8 * g);
+          sacc = mfma32(qa, kb, sacc);
+          dpacc = mfma32(da, vb, dpacc);
         }
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-          const int qq = 32 * qs + acc_row(i, g);
-          const float pv = fast_exp2(fmaf(sacc[i], c, -sm.lse2[qq]));
-          sacc[i] = pv;                                  // P
-          dpacc[i] = pv * (dpacc[i] - sm.delta[qq]);     // dS
+          const int qr = 32 * qs + acc_row(i, g);
+          const float pv = fast_exp2(fmaf(sacc[i], c, -sm.t.lse2[qr]));
+          sacc[i] = pv;                                    // P
+          dpacc[i] = pv * (dpacc[i] - sm.t.delta[qr]);     // dS
         }
         // dV^T += dO^T P, dK^T += Q^T dS (contraction over the 32 queries).
 #pragma unroll
@@ -197,8 +207,8 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkdv_kernel(BwdParams p) {
           const bf16x8 sb = pack_half(dpacc, h2);
 #pragma unroll
           for (int dt = 0; dt < DT; ++dt) {
-            const bf16x8 doa = lds_col8<D>(sm.dout, 32 * qs + 16 * h2, 8, 32 * dt, lane);
-            const bf16x8 qa = lds_col8<D>(sm.q, 32 * qs + 16 * h2, 8, 32 * dt, lane);
+            const bf16x8 doa = lds_col8<D>(sm.t.dout, 32 * qs + 16 * h2, 32 * dt, lane);
+            const bf16x8 qa = lds_col8<D>(sm.t.q, 32 * qs + 16 * h2, 32 * dt, lane);
             dvacc[dt] = mfma32(doa, pb, dvacc[dt]);
             dkacc[dt] = mfma32(qa, sb, dkacc[dt]);
           }
@@ -207,11 +217,36 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkdv_kernel(BwdParams p) {
     }
   }
 
-  if (kvalid) {
+  // Sum the two query halves (qh = 1 hands its partials to qh = 0), dK then dV.
+  __syncthreads();
+  if (qh == 1) {
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) sm.red[kw][dt][i][lane] = dkacc[dt][i];
+  }
+  __syncthreads();
+  if (qh == 0) {
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) dkacc[dt][i] += sm.red[kw][dt][i][lane];
+  }
+  __syncthreads();
+  if (qh == 1) {
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) sm.red[kw][dt][i][lane] = dvacc[dt][i];
+  }
+  __syncthreads();
+  if (qh == 0 && kvalid) {
     __bf16* dkp = p.dk + b * p.dk_sb + hk * p.dk_sh + (int64_t)key * p.dk_st;
     __bf16* dvp = p.dv + b * p.dv_sb + hk * p.dv_sh + (int64_t)key * p.dv_st;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) dvacc[dt][i] += sm.red[kw][dt][i][lane];
       store_acc_t(dkp, dkacc[dt], 32 * dt, g, p.scale);
       store_acc_t(dvp, dvacc[dt], 32 * dt, g, 1.f);
     }
@@ -220,8 +255,8 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dkdv_kernel(BwdParams p) {
 
 template <int D>
 struct DqSmem {
-  __bf16 k[kTile * D];  // swizzled rows (lds_off)
-  __bf16 v[kTile * D];
+  __bf16 k[kTile * pitch<D>()];  // padded rows
+  __bf16 v[kTile * pitch<D>()];
 };
 
 // dQ for one (b, query head, 128-query tile).  Per wave 32 queries; S^T and
@@ -296,16 +331,16 @@ __global__ __launch_bounds__(kThreads, 2) void bwd_dq_kernel(BwdParams p) {
       const bool mixed = __ballot(w4[j] != ~0u) != 0ull;
       f32x16 sacc, dpacc;
       {
-        const bf16x8 ka = lds_row8<D>(sm.k, 32 * j + n, 8 * g);
-        const bf16x8 va = lds_row8<D>(sm.v, 32 * j + n, 8 * g);
-        if (mixed) sacc = mfma32(ka, qf[0], mask_bias(w4[j] >> (4 * g)));
+        const bf16x8 ka = lds_row8<D>(sm.k, 32 * j + tok_perm(n), 8 * g);
+        const bf16x8 va = lds_row8<D>(sm.v, 32 * j + tok_perm(n), 8 * g);
+        if (mixed) sacc = mfma32(ka, qf[0], mask_bias(w4[j] >> g));
         else sacc = mfma32(ka, qf[0], f32x16{});
         dpacc = mfma32(va, dof[0], f32x16{});
       }
 #pragma unroll
       for (int s = 1; s < KS; ++s) {
-        const bf16x8 ka = lds_row8<D>(sm.k, 32 * j + n, 16 * s + 8 * g);
-        const bf16x8 va = lds_row8<D>(sm.v, 32 * j + n, 16 * s + 8 * g);
+        const bf16x8 ka = lds_row8<D>(sm.k, 32 * j + tok_perm(n), 16 * s + 8 * g);
+        const bf16x8 va = lds_row8<D>(sm.v, 32 * j + tok_perm(n), 16 * s + 8 * g);
         sacc = mfma32(ka, qf[s], sacc);
         dpacc = mfma32(va, dof[s], dpacc);
       }
@@ -320,7 +355,7 @@ __global__ __launch_bounds__(kThreads, 2) void bwd_dq_kernel(BwdParams p) {
         const bf16x8 sb = pack_half(dpacc, h2);
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) {
-          const bf16x8 ka = lds_col8<D>(sm.k, 32 * j + 16 * h2, 8, 32 * dt, lane);
+          const bf16x8 ka = lds_col8<D>(sm.k, 32 * j + 16 * h2, 32 * dt, lane);
           dqacc[dt] = mfma32(ka, sb, dqacc[dt]);
         }
       }
@@ -378,8 +413,8 @@ hipError_t launch_attn_bwd_phase(int phase, const TensorView& q, const TensorVie
     else hipLaunchKernelGGL(bwd_delta_kernel<128>, grid, dim3(kThreads), 0, stream, p);
   } else if (phase == kBwdDkDv) {
     const dim3 grid(dims.Hkv, nt, dims.B);
-    if (d64) hipLaunchKernelGGL(bwd_dkdv_kernel<64>, grid, dim3(kThreads), 0, stream, p);
-    else hipLaunchKernelGGL(bwd_dkdv_kernel<128>, grid, dim3(kThreads), 0, stream, p);
+    if (d64) hipLaunchKernelGGL(bwd_dkdv_kernel<64>, grid, dim3(kDkdvThreads), 0, stream, p);
+    else hipLaunchKernelGGL(bwd_dkdv_kernel<128>, grid, dim3(kDkdvThreads), 0, stream, p);
   } else {
     const dim3 grid(dims.Hq, nt, dims.B);
     if (d64) hipLaunchKernelGGL(bwd_dq_kernel<64>, grid, dim3(kThreads), 0, stream, p);

@@ -11,8 +11,9 @@
 //
 // Formulation (per wave, 32 queries):  S^T = K Q^T  so that every lane owns a
 // single query column (row max / row sum need one cross-half exchange), then
-// O^T += V^T P^T with P^T fed straight from the S^T accumulators and V^T read
-// from the row-major LDS tile by transpose loads.  The softmax runs in the
+// O^T += V^T P^T with P^T fed straight from the S^T accumulators (keys in
+// tok_perm order) and V^T read from the row-major LDS tile by transpose loads
+// in the same key order.  The softmax runs in the
 // log2 domain (scores times scale * log2 e); LSE is written in that domain,
 // and the host multiplies by ln 2 for the natural-log value.
 //
@@ -27,8 +28,8 @@ namespace {
 
 template <int D>
 struct FwdSmem {
-  __bf16 k[kTile * D];  // swizzled rows (lds_off)
-  __bf16 v[kTile * D];
+  __bf16 k[kTile * pitch<D>()];  // padded rows
+  __bf16 v[kTile * pitch<D>()];
 };
 
 struct FwdParams {
@@ -109,64 +110,73 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(FwdParams p)
       mixed[j] = __ballot(w4[j] != ~0u) != 0ull;
     }
 
-    // S^T (4 blocks of 32 keys) = K Q^T (+ mask bias).
-    f32x16 st[4];
+    // The tile is processed as two 64-key halves, each a complete online
+    // softmax step; this bounds the live score registers to 32 per lane.
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      if (!act[j]) continue;
-      const bf16x8 kf0 = lds_row8<D>(sm.k, 32 * j + n, 8 * g);
-      if (mixed[j]) st[j] = mfma32(kf0, qf[0], mask_bias(w4[j] >> (4 * g)));
-      else st[j] = mfma32(kf0, qf[0], f32x16{});
+    for (int half = 0; half < 2; ++half) {
+      const int j0 = 2 * half;
+      if (!act[j0] && !act[j0 + 1]) continue;
+      // S^T (2 blocks of 32 keys) = K Q^T (+ mask bias).
+      f32x16 st[2];
 #pragma unroll
-      for (int s = 1; s < KS; ++s) {
-        const bf16x8 kf = lds_row8<D>(sm.k, 32 * j + n, 16 * s + 8 * g);
-        st[j] = mfma32(kf, qf[s], st[j]);
+      for (int jj = 0; jj < 2; ++jj) {
+        const int j = j0 + jj;
+        if (!act[j]) continue;
+        const bf16x8 kf0 = lds_row8<D>(sm.k, 32 * j + tok_perm(n), 8 * g);
+        if (mixed[j]) st[jj] = mfma32(kf0, qf[0], mask_bias(w4[j] >> g));
+        else st[jj] = mfma32(kf0, qf[0], f32x16{});
+#pragma unroll
+        for (int s = 1; s < KS; ++s) {
+          const bf16x8 kf = lds_row8<D>(sm.k, 32 * j + tok_perm(n), 16 * s + 8 * g);
+          st[jj] = mfma32(kf, qf[s], st[jj]);
+        }
       }
-    }
 
-    float mx = -INFINITY;
+      float mx = -INFINITY;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      if (!act[j]) continue;
+      for (int jj = 0; jj < 2; ++jj) {
+        if (!act[j0 + jj]) continue;
 #pragma unroll
-      for (int i = 0; i < 16; ++i) mx = fmaxf(mx, st[j][i]);
-    }
-    mx = halves_max(mx);
-    const float m_new = fmaxf(m_run, mx);
-    const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
-    const float neg = -m_use * c;
-    float rs = 0.f;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      if (!act[j]) continue;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const float e = fast_exp2(fmaf(st[j][i], c, neg));
-        st[j][i] = e;
-        rs += e;
+        for (int i = 0; i < 16; ++i) mx = fmaxf(mx, st[jj][i]);
       }
-    }
-    rs = halves_sum(rs);
-    // Rescale O only when some lane's running max moved (alpha == 1 otherwise).
-    if (__ballot(m_new != m_run) != 0ull) {
-      const float alpha = fast_exp2((m_run - m_use) * c);
-      l_run *= alpha;
+      mx = halves_max(mx);
+      const float m_new = fmaxf(m_run, mx);
+      const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
+      const float neg = -m_use * c;
+      float rs = 0.f;
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt) oacc[dt] *= alpha;
-    }
-    l_run += rs;
-    m_run = m_new;
+      for (int jj = 0; jj < 2; ++jj) {
+        if (!act[j0 + jj]) continue;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const float e = fast_exp2(fmaf(st[jj][i], c, neg));
+          st[jj][i] = e;
+          rs += e;
+        }
+      }
+      rs = halves_sum(rs);
+      // Rescale O only when some lane's running max moved (alpha == 1 otherwise).
+      if (__ballot(m_new != m_run) != 0ull) {
+        const float alpha = fast_exp2((m_run - m_use) * c);
+        l_run *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) oacc[dt] *= alpha;
+      }
+      l_run += rs;
+      m_run = m_new;
 
-    // O^T += V^T P^T, 16 keys per k-step.
+      // O^T += V^T P^T, 16 keys per k-step.
 #pragma unroll
-    for (int s = 0; s < 8; ++s) {
-      const int j = s >> 1, hh = s & 1;
-      if (!act[j]) continue;
-      const bf16x8 pf = pack_half(st[j], hh);
+      for (int s = 0; s < 4; ++s) {
+        const int jj = s >> 1, hh = s & 1;
+        const int j = j0 + jj;
+        if (!act[j]) continue;
+        const bf16x8 pf = pack_half(st[jj], hh);
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt) {
-        const bf16x8 vf = lds_col8<D>(sm.v, 32 * j + 16 * hh, 8, 32 * dt, lane);
-        oacc[dt] = mfma32(vf, pf, oacc[dt]);
+        for (int dt = 0; dt < DT; ++dt) {
+          const bf16x8 vf = lds_col8<D>(sm.v, 32 * j + 16 * hh, 32 * dt, lane);
+          oacc[dt] = mfma32(vf, pf, oacc[dt]);
+        }
       }
     }
   }

@@ -1,20 +1,26 @@
 // Shared device helpers for the gfx950 masked-attention kernels.
 //
 // Tile geometry: the BlockMask granularity is 128 x 128 (the reference's
-// create_block_mask default, torch/nn/attention/flex_attention.py:395).  Every
-// attention work-group owns one 128-token tile and runs 4 waves of 64 lanes;
-// each wave owns 32 rows of that tile.  All dense contractions use the CDNA4
-// v_mfma_f32_32x32x16_bf16 instruction, whose lane layout is
+// create_block_mask default, torch/nn/attention/flex_attention.py:395).  All
+// dense contractions use the CDNA4 v_mfma_f32_32x32x16_bf16 instruction, whose
+// lane layout is
 //   A (32x16, M x K): lane l holds A[l % 32][8 * (l / 32) + j], j = 0..7
 //   B (16x32, K x N): lane l holds B[8 * (l / 32) + j][l % 32]
 //   C (32x32, f32):   lane l, acc i holds C[8 * (i / 4) + 4 * (l / 32) + i % 4][l % 32]
-// Operand tiles live row-major in LDS ([token][d], d contiguous, no padding)
-// with the 16-byte chunks of row r XOR-permuted by swz(r), so that both read
-// patterns below hit distinct banks.  A "row" operand (contraction over d) is
-// one 16-byte ds_read_b128 per lane (16 lanes read 16 rows of one chunk); a
-// "column" operand (contraction over tokens) is two ds_read_b64_tr_b16 reads,
-// whose result in each 16-lane group is out[i][j] = mem[addr[4 j + i / 4] + i % 4]
-// (4 rows x 32 bytes per 16 lanes).
+//
+// LDS tiles are row-major [token][d] with rows padded by 16 bytes (pitch
+// D + 8 elements).  A "row" operand (contraction over d) is one 16-byte
+// ds_read_b128 per lane; a "column" operand (contraction over tokens) is two
+// ds_read_b64_tr_b16 reads, whose result in each 16-lane group is
+// out[i][j] = mem[addr[4 j + i / 4] + i % 4].
+//
+// The first contraction of every kernel puts tokens on the MFMA M side.  Its
+// A-operand lane m reads token tok_perm(m) of the 32-token block instead of
+// token m, so accumulator row m holds token tok_perm(m).  The permutation is
+// chosen so that each column read touches rows four apart: with the 16-byte
+// row padding, the 16 rows of a row read and the 4 x 64 bytes of a 32-lane
+// column read then fall on distinct LDS banks, while every address stays a
+// per-lane base plus an immediate offset.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -41,39 +47,46 @@ __device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
-// Chunk permutation of LDS row r for a D-wide bf16 tile: rows r .. r+15 map a
-// given chunk to 16 distinct positions, and rows 4a .. 4a+3 map the chunk
-// pairs (2m, 2m+1), (2m+2, 2m+3) to distinct positions.
+// LDS row pitch (elements) of a D-wide bf16 tile.
 template <int D>
-__device__ __forceinline__ constexpr int swz(int r) {
-  return (4 * (r & 3) + ((r >> 2) & 3)) & (D / 8 - 1);
+__device__ __forceinline__ constexpr int pitch() { return D + 8; }
+
+// Token of A-operand row m (0..31) within a 32-token block:
+// m = 16 h + 8 b + 4 g + r  ->  16 h + 4 r + 2 b + g.
+__device__ __forceinline__ constexpr int tok_perm(int m) {
+  return 16 * (m >> 4) + 4 * (m & 3) + 2 * ((m >> 3) & 1) + ((m >> 2) & 1);
 }
 
-// Element offset of (row r, column col) in a swizzled LDS tile.
-template <int D>
-__device__ __forceinline__ int lds_off(int r, int col) {
-  return r * D + ((((col >> 3) ^ swz<D>(r))) << 3) + (col & 7);
+// Token of accumulator entry i of lane group g (tok_perm of its C row).
+__device__ __forceinline__ constexpr int acc_tok(int i, int g) {
+  return 16 * (i >> 3) + 4 * (i & 3) + 2 * ((i >> 2) & 1) + g;
+}
+
+// Bit of accumulator entry i in a bitmap word already shifted right by g.
+__device__ __forceinline__ constexpr int acc_tok_bit(int i) {
+  return 16 * (i >> 3) + 4 * (i & 3) + 2 * ((i >> 2) & 1);
 }
 
 // Row operand: 8 consecutive bf16 (col a multiple of 8) of row r.
 template <int D>
 __device__ __forceinline__ bf16x8 lds_row8(const __bf16* tile, int r, int col) {
-  return *reinterpret_cast<const bf16x8*>(tile + lds_off<D>(r, col));
+  return *reinterpret_cast<const bf16x8*>(tile + r * pitch<D>() + col);
 }
 
-// Column operand for the A or B slot of mfma32: lane (g = l/32, c = l%32)
-// receives tile[r0 + j][col0 + c] for j = 0..3 and tile[r1 + j][col0 + c] for
-// j = 4..7, where r0 = base_row + 4 g, r1 = r0 + second_off.
+// Column operand (A or B slot of mfma32) over the 16 tokens [base, base + 16)
+// of a block, in accumulator order: lane (g = l/32, c = l%32) receives
+// tile[base + g + 4 j][col0 + c] for j = 0..3 and tile[base + 2 + g + 4 j][col0 + c]
+// for j = 4..7, i.e. the tokens acc_tok(8 h + j, g) - 16 h of a half h whose
+// first token is base.
 template <int D>
-__device__ __forceinline__ bf16x8 lds_col8(const __bf16* tile, int base_row, int second_off,
-                                           int col0, int lane) {
+__device__ __forceinline__ bf16x8 lds_col8(const __bf16* tile, int base, int col0, int lane) {
   const int grp = lane >> 4;                 // 16-lane group 0..3
   const int r = lane & 15;                   // lane within group
   const int g = grp >> 1;                    // k-group of the MFMA operand
   const int c = col0 + 16 * (grp & 1) + 4 * (r & 3);
-  const int row = base_row + 4 * g + (r >> 2);
-  const __bf16* p0 = tile + lds_off<D>(row, c);
-  const __bf16* p1 = tile + lds_off<D>(row + second_off, c);
+  const int row = base + g + 4 * (r >> 2);
+  const __bf16* p0 = tile + row * pitch<D>() + c;
+  const __bf16* p1 = p0 + 2 * pitch<D>();
   bf16x4_ld lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4_ptr)(p0));
   bf16x4_ld hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4_ptr)(p1));
   return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
@@ -110,13 +123,14 @@ __device__ __forceinline__ float halves_sum(float x) {
 }
 
 // MFMA accumulator seed for a mixed 32x32 block: 0 where the pair is allowed,
-// -inf where it is masked.  `sw` is the lane's bitmap word shifted right by 4 g.
+// -inf where it is masked.  `sw` is the lane's bitmap word (bit t = token t
+// of the block) shifted right by the lane group g.
 __device__ __forceinline__ f32x16 mask_bias(uint32_t sw) {
   f32x16 c;
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     // bit set -> keep = 0 -> +0.0; bit clear -> keep = ~0 -> 0xff800000 = -inf
-    const uint32_t keep = ((sw >> (8 * (i >> 2) + (i & 3))) & 1u) - 1u;
+    const uint32_t keep = ((sw >> acc_tok_bit(i)) & 1u) - 1u;
     c[i] = __uint_as_float(keep & 0xff800000u);
   }
   return c;
@@ -135,33 +149,29 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t slice_rsrc(const __bf16* base,
                                            0x00020000);
 }
 
-// Copy token rows [t0, t0 + 128) of a slice into a swizzled LDS tile; rows
+// Copy token rows [t0, t0 + 128) of a slice into a padded LDS tile; rows
 // past the slice end read as zeros.  Each thread moves 16-byte chunks; a wave
 // covers four whole rows.
-template <int D>
+template <int D, int NTHREADS = kThreads>
 __device__ __forceinline__ void load_tile_lds(__bf16* dst, __amdgpu_buffer_rsrc_t src,
                                               int64_t st, int t0, int tid) {
   constexpr int kChunks = D / 8;
-  constexpr int kIters = kTile * kChunks / kThreads;
+  constexpr int kIters = kTile * kChunks / NTHREADS;
   const int soff = (int)((int64_t)t0 * st * 2);
   uint4 buf[kIters];
 #pragma unroll
   for (int it = 0; it < kIters; ++it) {
-    const int c = tid + it * kThreads;
+    const int c = tid + it * NTHREADS;
     const int r = c / kChunks, col = (c % kChunks) * 8;
     buf[it] = __builtin_bit_cast(
         uint4, __builtin_amdgcn_raw_buffer_load_b128(src, (int)((r * st + col) * 2), soff, 0));
   }
 #pragma unroll
   for (int it = 0; it < kIters; ++it) {
-    const int c = tid + it * kThreads;
+    const int c = tid + it * NTHREADS;
     const int r = c / kChunks, col = (c % kChunks) * 8;
-    *reinterpret_cast<uint4*>(dst + lds_off<D>(r, col)) = buf[it];
+    *reinterpret_cast<uint4*>(dst + r * pitch<D>() + col) = buf[it];
   }
 }
-
-// Bit of a tile-bitmap word for accumulator entry i, after the word has been
-// shifted right by 4 * g (entries 8 c + r, c = i / 4, r = i % 4).
-__device__ __forceinline__ constexpr int acc_bit(int i) { return 8 * (i >> 2) + (i & 3); }
 
 }  // namespace t2t
