@@ -202,11 +202,18 @@ int t2t_attn_bwd(const t2t_tensor* q, const t2t_tensor* k, const t2t_tensor* v,
                  const t2t_tensor* o, const t2t_tensor* dout, const float* lse2,
                  float* delta, const t2t_tensor* dq, const t2t_tensor* dk,
                  const t2t_tensor* dv, int32_t B, int32_t Hq, int32_t Hkv, int32_t T,
-                 int32_t D, int32_t dtype, float scale, const t2t_block_mask* mask, void* stream) {
+                 int32_t D, int32_t dtype, float scale, const t2t_block_mask* mask,
+                 void* stream) {
+  // Validate every argument of the three phases before launching any of them.
   int rc = check_dims(B, Hq, Hkv, T, D, dtype);
   if (rc) return rc;
   if (B == 0 || Hq == 0 || T == 0) return T2T_OK;
-  if (!view_ok(o)) return fail(T2T_EINVAL, "o view invalid");
+  if (!view_ok(q) || !view_ok(k) || !view_ok(v) || !view_ok(o) || !view_ok(dout) ||
+      !view_ok(dq) || !view_ok(dk) || !view_ok(dv))
+    return fail(T2T_EINVAL, "tensor view invalid (NULL, misaligned or bad stride)");
+  if (!lse2 || !delta) return fail(T2T_EINVAL, "lse2/delta is NULL");
+  rc = check_mask(mask, B, T, true, true);
+  if (rc) return rc;
   rc = t2t_attn_bwd_preprocess(o, dout, delta, B, Hq, T, D, dtype, stream);
   if (rc) return rc;
   rc = t2t_attn_bwd_dkdv(q, k, v, dout, lse2, delta, dk, dv, B, Hq, Hkv, T, D, dtype, scale,

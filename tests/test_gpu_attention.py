@@ -128,3 +128,23 @@ def test_full_size_against_torch_fp32(cfg, gpu_device):
     for (b, hk), dk_ref in ref["dk"].items():
         assert_close(k.grad[b, hk], dk_ref, ATOL, RTOL, f"cfg{cfg} dk b{b} hk{hk}")
         assert_close(v.grad[b, hk], ref["dv"][(b, hk)], ATOL, RTOL, f"cfg{cfg} dv b{b} hk{hk}")
+
+
+@pytest.mark.parametrize("name", ["cross_doc_link_T130_gqa", "doc_causal_T96_d128"])
+def test_golden_fixture(name, gpu_device):
+    import os
+    f = np.load(os.path.join(os.path.dirname(__file__), "golden", f"attn_{name}.npz"))
+    qb = f["q_bits"] if "q_bits" in f else None
+    kb = f["kv_bits"] if "kv_bits" in f else None
+    bm = build_block_mask(torch.from_numpy(f["doc"]).to(gpu_device), to_dev_words(qb, gpu_device),
+                          to_dev_words(kb, gpu_device))
+    def dev(n):
+        return torch.from_numpy(f[n].view(np.int16)).view(torch.bfloat16).to(gpu_device)
+    q, k, v, do = dev("q"), dev("k"), dev("v"), dev("do")
+    q.requires_grad_(True); k.requires_grad_(True); v.requires_grad_(True)
+    out, lse = flex_attention(q, k, v, block_mask=bm, enable_gqa=q.shape[1] != k.shape[1],
+                              return_lse=True)
+    out.backward(do)
+    for got, ref in ((out, "o"), (q.grad, "dq"), (k.grad, "dk"), (v.grad, "dv")):
+        assert_close(got.detach(), torch.from_numpy(f[ref].astype(np.float32)), ATOL, RTOL, f"{name} {ref}")
+    assert_close(lse.detach(), torch.from_numpy(f["lse"]), 1e-3, 1e-3, f"{name} lse")

@@ -138,3 +138,16 @@ def test_deterministic(gpu_device):
     nt = a.num_tiles
     valid = torch.arange(nt, device=a.q_num_blocks.device)[None, None, :] < a.q_num_blocks[:, 0, :, None]
     assert torch.equal(a.q_bits_slot[valid], b.q_bits_slot[valid])
+
+
+@pytest.mark.parametrize("name", ["config1_T1024", "config3_T4096", "config4_T4096"])
+def test_golden_fixture(name, gpu_device):
+    import os
+    f = np.load(os.path.join(os.path.dirname(__file__), "golden", f"mask_{name}.npz"))
+    qb = f["q_bits"] if "q_bits" in f else None
+    kb = f["kv_bits"] if "kv_bits" in f else None
+    bm = build_block_mask(torch.from_numpy(f["doc"]).to(gpu_device), to_dev_words(qb, gpu_device),
+                          to_dev_words(kb, gpu_device))
+    np.testing.assert_array_equal(bm.tile_class[0].cpu().numpy(), f["tile_class"])
+    for n in TABLES:
+        np.testing.assert_array_equal(getattr(bm, n)[0, 0].cpu().numpy(), f[n], err_msg=n)

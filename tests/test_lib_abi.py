@@ -1,0 +1,106 @@
+"""The C-ABI library loads, exports every symbol include/t2t_attn.h declares,
+and rejects bad arguments before touching the GPU; the Python layer refuses
+CPU tensors (there is no CPU fallback)."""
+import ctypes
+import os
+
+import pytest
+import torch
+
+from tagseq2tagseq_amd import _lib
+
+
+def test_library_built_and_loads():
+    assert os.path.exists(_lib.LIB_PATH), "run python -m tagseq2tagseq_amd.build"
+    assert b"gfx950" in _lib.lib().t2t_version()
+
+
+def test_exports_every_header_symbol():
+    names = _lib.header_functions()
+    assert {"t2t_mask_meta", "t2t_attn_fwd", "t2t_attn_bwd", "t2t_attn_bwd_preprocess",
+            "t2t_attn_bwd_dkdv", "t2t_attn_bwd_dq", "t2t_last_error", "t2t_version"} <= set(names)
+    lib = _lib.lib()
+    for n in names:
+        assert hasattr(lib, n), n
+
+
+# The argument-check tests pass placeholder device pointers that the library
+# must reject before any launch; they run only where no GPU is visible.
+no_gpu = pytest.mark.skipif(torch.cuda.is_available(),
+                            reason="placeholder-pointer checks run on CPU-only hosts")
+
+
+def _dummy_view():
+    return _lib.T2TTensor(0x1000, 0, 0, 128)
+
+
+def _err():
+    return _lib.lib().t2t_last_error().decode()
+
+
+@no_gpu
+def test_fwd_rejects_unsupported_head_dim():
+    v = _dummy_view()
+    m = _lib.T2TBlockMaskC()
+    rc = _lib.lib().t2t_attn_fwd(ctypes.byref(v), ctypes.byref(v), ctypes.byref(v), ctypes.byref(v),
+                                 ctypes.c_void_p(0x1000), 1, 2, 2, 256, 96, 0, 0.1,
+                                 ctypes.byref(m), None)
+    assert rc == -2 and "head dim" in _err()
+
+
+@no_gpu
+def test_fwd_rejects_bad_gqa_and_dtype():
+    v = _dummy_view()
+    m = _lib.T2TBlockMaskC()
+    lib = _lib.lib()
+    rc = lib.t2t_attn_fwd(*[ctypes.byref(v)] * 4, ctypes.c_void_p(0x1000), 1, 3, 2, 256, 128, 0,
+                          0.1, ctypes.byref(m), None)
+    assert rc == -1 and "GQA" in _err()
+    rc = lib.t2t_attn_fwd(*[ctypes.byref(v)] * 4, ctypes.c_void_p(0x1000), 1, 2, 2, 256, 128, 7,
+                          0.1, ctypes.byref(m), None)
+    assert rc == -2 and "dtype" in _err()
+
+
+@no_gpu
+def test_bwd_rejects_null_mask():
+    v = _dummy_view()
+    rc = _lib.lib().t2t_attn_bwd(*[ctypes.byref(v)] * 5, ctypes.c_void_p(0x1000),
+                                 ctypes.c_void_p(0x1000), *[ctypes.byref(v)] * 3,
+                                 1, 2, 2, 256, 128, 0, 0.1, None, None)
+    assert rc == -1 and "mask" in _err()
+
+
+@no_gpu
+def test_mask_meta_argument_checks():
+    lib = _lib.lib()
+    out = _lib.T2TBlockMaskC(1, 2)
+    assert lib.t2t_mask_meta(None, None, None, 1, 0, 0, None, ctypes.byref(out), None) == 0  # T = 0
+    assert lib.t2t_mask_meta(None, None, None, 1, 256, 9, None, ctypes.byref(out), None) == -2
+    assert "words" in _err()
+    # capacity check: 2 tiles need 3 bitmap slots
+    out.tile_bits_slots = 2
+    rc = lib.t2t_mask_meta(ctypes.c_void_p(0x1000), None, None, 1, 256, 0, ctypes.c_void_p(0x1000),
+                           ctypes.byref(out), None)
+    assert rc == -1 and "slots" in _err()
+    out = _lib.T2TBlockMaskC(1, 3, tile_bits_slots=100)
+    rc = lib.t2t_mask_meta(ctypes.c_void_p(0x1000), None, None, 1, 256, 0, ctypes.c_void_p(0x1000),
+                           ctypes.byref(out), None)
+    assert rc == -1 and "nt=" in _err()
+
+
+def test_python_layer_refuses_cpu_tensors():
+    from tagseq2tagseq_amd.block_mask import build_block_mask
+    from tagseq2tagseq_amd.mask_creators import create_doc_causal_block_mask
+    with pytest.raises(RuntimeError, match="GPU"):
+        build_block_mask(torch.zeros(256, dtype=torch.int32))
+    with pytest.raises(RuntimeError, match="GPU"):
+        create_doc_causal_block_mask(torch.zeros((1, 256), dtype=torch.long), [])
+
+
+def test_flex_attention_validation_on_cpu():
+    from tagseq2tagseq_amd.attention import flex_attention
+    q = torch.zeros(1, 2, 256, 128, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="block_mask is required"):
+        flex_attention(q, q, q)
+    with pytest.raises(NotImplementedError):
+        flex_attention(q, q, q, score_mod=lambda s, b, h, i, j: s, block_mask=object())
