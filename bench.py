@@ -81,6 +81,22 @@ def count_pairs(doc, qb, kb, chunk=1024) -> int:
     return total
 
 
+def measured_traffic(config: int, kernel: str):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 summary
+    (profiles/hbm_traffic_config<N>.txt: FETCH_SIZE / WRITE_SIZE passes scaled
+    by the copy calibration), or None when no summary exists."""
+    path = os.path.join(ROOT, "profiles", f"hbm_traffic_config{config}.txt")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        for line in f:
+            if line.startswith(kernel + ":"):
+                for tok in line.split():
+                    if tok.startswith("traffic_bytes="):
+                        return int(tok.split("=", 1)[1])
+    return None
+
+
 def time_launches(fn, reps: int) -> float:
     """Mean duration (ms) of fn()'s launches, HIP events on the current stream."""
     start = torch.cuda.Event(enable_timing=True)
@@ -263,7 +279,8 @@ def main():
             "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(args.config, dom),
+            "traffic_source": f"profiles/hbm_traffic_config{args.config}.txt",
         },
         "kernels_ms": {
             "mask_meta (4 launches)": round(t_meta, 4),
