@@ -180,7 +180,7 @@ __global__ __launch_bounds__(kDkdvThreads, 1) void bwd_dkdv_kernel(BwdParams p) 
           const bf16x8 da = lds_row8<D>(sm.t.dout, 32 * qs + tok_perm(n), 8 * g);
           const bf16x8 kb = lds_row8<D>(sm.k, kloc, 8 * g);
           const bf16x8 vb = lds_row8<D>(sm.v, kloc, 8 * g);
-          if (mixed) sacc = mfma32(qa, kb, mask_bias(w2[qq] >> g));
+          if (mixed) sacc = mfma32(qa, kb, mask_bias(~(w2[qq] >> g)));
           else sacc = mfma32(qa, kb, f32x16{});
           dpacc = mfma32(da, vb, f32x16{});
         }
@@ -333,7 +333,7 @@ __global__ __launch_bounds__(kThreads, 2) void bwd_dq_kernel(BwdParams p) {
       {
         const bf16x8 ka = lds_row8<D>(sm.k, 32 * j + tok_perm(n), 8 * g);
         const bf16x8 va = lds_row8<D>(sm.v, 32 * j + tok_perm(n), 8 * g);
-        if (mixed) sacc = mfma32(ka, qf[0], mask_bias(w4[j] >> g));
+        if (mixed) sacc = mfma32(ka, qf[0], mask_bias(~(w4[j] >> g)));
         else sacc = mfma32(ka, qf[0], f32x16{});
         dpacc = mfma32(va, dof[0], f32x16{});
       }

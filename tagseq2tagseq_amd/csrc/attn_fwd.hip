@@ -13,9 +13,18 @@
 // single query column (row max / row sum need one cross-half exchange), then
 // O^T += V^T P^T with P^T fed straight from the S^T accumulators (keys in
 // tok_perm order) and V^T read from the row-major LDS tile by transpose loads
-// in the same key order.  The softmax runs in the
-// log2 domain (scores times scale * log2 e); LSE is written in that domain,
-// and the host multiplies by ln 2 for the natural-log value.
+// in the same key order.  The softmax runs in the log2 domain (scores times
+// scale * log2 e); LSE is written in that domain, and the host multiplies by
+// ln 2 for the natural-log value.  The running reference max only moves when
+// a row's max exceeds it by more than 2^8 in probability (lazy rescaling):
+// probabilities stay below 256, far inside fp32 / bf16 range, and O is
+// rescaled a handful of times per row instead of at every block.
+//
+// Pipeline: each KV tile is consumed as two 64-key halves (K rows + V rows,
+// one LDS unit each).  While a wave computes on one half, the other half's
+// units are being filled by direct global->LDS copies issued right after the
+// barrier that retired them, together with the next tile's bitmap; one
+// barrier per half.  No staging registers and no register->LDS stores.
 //
 // Work-groups are dispatched longest row first (row_order) with the head as
 // the fastest grid dimension, so the heads sharing an XCD (blockIdx.x mod 8)
@@ -25,12 +34,6 @@
 namespace t2t {
 
 namespace {
-
-template <int D>
-struct FwdSmem {
-  __bf16 k[kTile * pitch<D>()];  // padded rows
-  __bf16 v[kTile * pitch<D>()];
-};
 
 struct FwdParams {
   const __bf16* q; int64_t q_sb, q_sh, q_st;
@@ -49,10 +52,13 @@ template <int D>
 __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(FwdParams p) {
   constexpr int KS = D / 16;  // MFMA k-steps over the head dim
   constexpr int DT = D / 32;  // 32-wide output column tiles
-  __shared__ FwdSmem<D> sm;
+  using U = UnitDma<D>;
+  constexpr int kUnit = U::kRows * pitch<D>();
+  __shared__ __bf16 k_lo[kUnit], k_hi[kUnit], v_lo[kUnit], v_hi[kUnit];
+  __shared__ uint32_t bits_lds[2][kTile * 4];
 
   const int h = blockIdx.x, b = blockIdx.z;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x, wave = uniform(tid >> 6), lane = tid & 63;
   const int g = lane >> 5, n = lane & 31;
   const int hk = h / (p.Hq / p.Hkv);
   const int mb = p.m.Bm > 1 ? b : 0;
@@ -75,110 +81,150 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(FwdParams p)
     }
   }
 
-  const auto krs = slice_rsrc(p.k + b * p.k_sb + hk * p.k_sh, p.k_st, T, D);
-  const auto vrs = slice_rsrc(p.v + b * p.v_sb + hk * p.v_sh, p.v_st, T, D);
+  const __bf16* kbase = p.k + b * p.k_sb + hk * p.k_sh;
+  const __bf16* vbase = p.v + b * p.v_sb + hk * p.v_sh;
+  int koff[U::kPerWave + 1], voff[U::kPerWave + 1];
+#pragma unroll
+  for (int j = 0; j < U::kPerWave; ++j) {
+    koff[j] = unit_dma_offset<D>(wave + kWaves * j, p.k_st, lane);
+    voff[j] = unit_dma_offset<D>(wave + kWaves * j, p.v_st, lane);
+  }
+  koff[U::kPerWave] = unit_dma_offset<D>(U::kInsts - 1, p.k_st, lane);
+  voff[U::kPerWave] = unit_dma_offset<D>(U::kInsts - 1, p.v_st, lane);
+
   const size_t row = (size_t)mb * nt + qt;
   const int npart = uniform(p.m.kv_num[row]);
   const int nfull = uniform(p.m.full_kv_num[row]);
+  const int ntiles = npart + nfull;
   const int32_t* pidx = p.m.kv_idx + row * nt;
   const int32_t* fidx = p.m.full_kv_idx + row * nt;
-  const uint32_t* bits_base = p.m.tile_bits + (size_t)p.m.kv_bits_off[row] * kTileBitsWords + qloc * 4;
+  const uint32_t* bits_row = p.m.tile_bits + (size_t)p.m.kv_bits_off[row] * kTileBitsWords;
+
+  // KV tile indices of the row, 64 iterations per chunk: lane j of tiles_v
+  // holds the tile of iteration 64 * chunk + j (read back with readlane).
+  auto load_chunk = [&](int chunk) {
+    const int it = 64 * chunk + lane;
+    return it < npart ? pidx[it] : (it < ntiles ? fidx[it - npart] : 0);
+  };
+  int tiles_v = load_chunk(0);
+  auto tile_of = [&](int it) { return __builtin_amdgcn_readlane(tiles_v, it & 63); };
+  // K and V rows [t0, t0 + 64) into one half's units.
+  auto load_half = [&](__bf16* kd, __bf16* vd, int t0) {
+    unit_dma<D>(kd, rows_rsrc(kbase, p.k_st, t0, T, D), koff, wave, 0);
+    unit_dma<D>(vd, rows_rsrc(vbase, p.v_st, t0, T, D), voff, wave, 1);
+  };
+  // Row-major half (128 queries x 4 words) of tile `it`'s bitmap slot; each
+  // wave copies 1 KiB (waves w and w + 2 copy the same bytes).
+  auto load_bits = [&](int it) {
+    const auto rs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint32_t*>(bits_row + (size_t)it * kTileBitsWords), 0, kTile * 16, 0x00020000);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        rs, (__attribute__((address_space(3))) void*)(&bits_lds[it & 1][(wave & 1) * 256]), 16,
+        (wave & 1) * 1024 + lane * 16, 0, 0, 0);
+  };
 
   f32x16 oacc[DT];
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) oacc[dt] = f32x16{};
-  float m_run = -INFINITY, l_run = 0.f;  // running max of raw scores, running sum
+  float m_ref = -INFINITY, l_run = 0.f;  // reference max of raw scores, running sum
 
-  for (int it = 0; it < npart + nfull; ++it) {
+  // One 64-key half: S^T = K Q^T (+ mask seed), lazy-rescaled online softmax,
+  // O^T += V^T P^T.  w0, w1: bitmap words of the half's two 32-key blocks.
+  auto half_step = [&](const __bf16* kt_lds, const __bf16* vt_lds, uint32_t w0, uint32_t w1,
+                       bool partial) {
+    const uint32_t w2[2] = {w0, w1};
+    bool act[2], mixed[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      act[j] = !partial || __ballot(w2[j] != 0u) != 0ull;
+      mixed[j] = partial && __ballot(w2[j] != ~0u) != 0ull;
+    }
+    if (!act[0] && !act[1]) return;
+    f32x16 st[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      if (!act[j]) continue;
+      const bf16x8 kf0 = lds_row8<D>(kt_lds, 32 * j + tok_perm(n), 8 * g);
+      if (mixed[j]) st[j] = mfma32(kf0, qf[0], mask_bias(~(w2[j] >> g)));
+      else st[j] = mfma32(kf0, qf[0], f32x16{});
+#pragma unroll
+      for (int s = 1; s < KS; ++s) {
+        const bf16x8 kf = lds_row8<D>(kt_lds, 32 * j + tok_perm(n), 16 * s + 8 * g);
+        st[j] = mfma32(kf, qf[s], st[j]);
+      }
+    }
+
+    float mx = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      if (!act[j]) continue;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) mx = fmaxf(mx, st[j][i]);
+    }
+    mx = halves_max(mx);
+    // The reference moves only when the row max exceeds it by 8 (log2
+    // units); -inf - -inf compares false, so untouched rows never move.
+    const bool move = (mx - m_ref) * c > 8.f;
+    if (__ballot(move) != 0ull) {
+      const float alpha = move ? fast_exp2((m_ref - mx) * c) : 1.f;  // 0 from -inf
+      l_run *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) oacc[dt] *= alpha;
+      m_ref = move ? mx : m_ref;
+    }
+    const float neg = m_ref == -INFINITY ? 0.f : -m_ref * c;
+    float rs = 0.f;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      if (!act[j]) continue;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const float e = fast_exp2(fmaf(st[j][i], c, neg));
+        st[j][i] = e;
+        rs += e;
+      }
+    }
+    l_run += halves_sum(rs);
+
+    // O^T += V^T P^T, 16 keys per k-step.
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const int j = s >> 1, hh = s & 1;
+      if (!act[j]) continue;
+      const bf16x8 pf = pack_half(st[j], hh);
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        const bf16x8 vf = lds_col8<D>(vt_lds, 32 * j + 16 * hh, 32 * dt, lane);
+        oacc[dt] = mfma32(vf, pf, oacc[dt]);
+      }
+    }
+  };
+
+  int k0_next = ntiles > 0 ? tile_of(0) * kTile : 0;
+  if (ntiles > 0) {
+    load_half(k_lo, v_lo, k0_next);
+    if (npart > 0) load_bits(0);
+  }
+  for (int it = 0; it < ntiles; ++it) {
     const bool partial = it < npart;
-    const int kt = uniform(partial ? pidx[it] : fidx[it - npart]);
-    const int k0 = kt * kTile;
+    const int k0 = k0_next;
+    // Keys [k0, k0 + 64): its units and bitmap have landed; the other half's
+    // units are free again.
+    dma_barrier();
+    load_half(k_hi, v_hi, k0 + 64);
     uint4 mbits = make_uint4(~0u, ~0u, ~0u, ~0u);
-    if (partial) mbits = *reinterpret_cast<const uint4*>(bits_base + (size_t)it * kTileBitsWords);
-    __syncthreads();
-    load_tile_lds<D>(sm.k, krs, p.k_st, k0, tid);
-    load_tile_lds<D>(sm.v, vrs, p.v_st, k0, tid);
-    __syncthreads();
+    if (partial) mbits = *reinterpret_cast<const uint4*>(&bits_lds[it & 1][qloc * 4]);
+    half_step(k_lo, v_lo, mbits.x, mbits.y, partial);
 
-    // 32-key blocks of this wave: empty (no allowed pair: skipped), full (no
-    // masking) or mixed (masked through the accumulator seed).  Wave-uniform.
-    const uint32_t w4[4] = {mbits.x, mbits.y, mbits.z, mbits.w};
-    bool act[4], mixed[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {  // full tiles carry all-ones words
-      act[j] = __ballot(w4[j] != 0u) != 0ull;
-      mixed[j] = __ballot(w4[j] != ~0u) != 0ull;
+    // Keys [k0 + 64, k0 + 128); the first half's units are free again.
+    dma_barrier();
+    if (it + 1 < ntiles) {
+      if (((it + 1) & 63) == 0) tiles_v = load_chunk((it + 1) >> 6);
+      k0_next = tile_of(it + 1) * kTile;
+      load_half(k_lo, v_lo, k0_next);
+      if (it + 1 < npart) load_bits(it + 1);
     }
-
-    // The tile is processed as two 64-key halves, each a complete online
-    // softmax step; this bounds the live score registers to 32 per lane.
-#pragma unroll
-    for (int half = 0; half < 2; ++half) {
-      const int j0 = 2 * half;
-      if (!act[j0] && !act[j0 + 1]) continue;
-      // S^T (2 blocks of 32 keys) = K Q^T (+ mask bias).
-      f32x16 st[2];
-#pragma unroll
-      for (int jj = 0; jj < 2; ++jj) {
-        const int j = j0 + jj;
-        if (!act[j]) continue;
-        const bf16x8 kf0 = lds_row8<D>(sm.k, 32 * j + tok_perm(n), 8 * g);
-        if (mixed[j]) st[jj] = mfma32(kf0, qf[0], mask_bias(w4[j] >> g));
-        else st[jj] = mfma32(kf0, qf[0], f32x16{});
-#pragma unroll
-        for (int s = 1; s < KS; ++s) {
-          const bf16x8 kf = lds_row8<D>(sm.k, 32 * j + tok_perm(n), 16 * s + 8 * g);
-          st[jj] = mfma32(kf, qf[s], st[jj]);
-        }
-      }
-
-      float mx = -INFINITY;
-#pragma unroll
-      for (int jj = 0; jj < 2; ++jj) {
-        if (!act[j0 + jj]) continue;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) mx = fmaxf(mx, st[jj][i]);
-      }
-      mx = halves_max(mx);
-      const float m_new = fmaxf(m_run, mx);
-      const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
-      const float neg = -m_use * c;
-      float rs = 0.f;
-#pragma unroll
-      for (int jj = 0; jj < 2; ++jj) {
-        if (!act[j0 + jj]) continue;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const float e = fast_exp2(fmaf(st[jj][i], c, neg));
-          st[jj][i] = e;
-          rs += e;
-        }
-      }
-      rs = halves_sum(rs);
-      // Rescale O only when some lane's running max moved (alpha == 1 otherwise).
-      if (__ballot(m_new != m_run) != 0ull) {
-        const float alpha = fast_exp2((m_run - m_use) * c);
-        l_run *= alpha;
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) oacc[dt] *= alpha;
-      }
-      l_run += rs;
-      m_run = m_new;
-
-      // O^T += V^T P^T, 16 keys per k-step.
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const int jj = s >> 1, hh = s & 1;
-        const int j = j0 + jj;
-        if (!act[j]) continue;
-        const bf16x8 pf = pack_half(st[jj], hh);
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) {
-          const bf16x8 vf = lds_col8<D>(sm.v, 32 * j + 16 * hh, 32 * dt, lane);
-          oacc[dt] = mfma32(vf, pf, oacc[dt]);
-        }
-      }
-    }
+    half_step(k_hi, v_hi, mbits.z, mbits.w, partial);
   }
 
   if (qvalid) {
@@ -196,7 +242,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(FwdParams p)
     }
     if (g == 0)
       p.lse2[((size_t)b * p.Hq + h) * T + qrow] =
-          l_run > 0.f ? m_run * c + __log2f(l_run) : -INFINITY;
+          l_run > 0.f ? m_ref * c + __log2f(l_run) : -INFINITY;
   }
 }
 

@@ -62,6 +62,68 @@ __device__ __forceinline__ constexpr int acc_tok(int i, int g) {
   return 16 * (i >> 3) + 4 * (i & 3) + 2 * ((i >> 2) & 1) + g;
 }
 
+// Buffer resource over rows [t0, T) of a [T, D] slice (row stride `st`
+// elements).  The range check of a raw buffer load covers the per-lane
+// offset, so rows at or past T read as zeros whatever the tile position.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_rsrc(const __bf16* base, int64_t st,
+                                                             int t0, int T, int D) {
+  const int64_t rows = (int64_t)T - t0;
+  const int64_t bytes = rows > 0 ? ((rows - 1) * st + D) * 2 : 0;
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<__bf16*>(base + (rows > 0 ? (int64_t)t0 * st : 0)), 0,
+                                           (int)(bytes < 0x7fffffff ? bytes : 0x7fffffff),
+                                           0x00020000);
+}
+
+// Direct global -> LDS copies (buffer_load ... lds, no staging registers) of
+// 64 token rows into a padded LDS unit [64][D + 8].  One instruction moves 64
+// lanes x 16 bytes into 64 consecutive 16-byte LDS slots; a padded row is
+// kSlots = D / 8 + 1 slots (the last one is the pad, loaded from an offset past
+// any buffer so that it reads zero and touches no memory), so a unit is exactly
+// kSlots instructions.  Instruction i, lane l covers slot 64 i + l.
+template <int D>
+struct UnitDma {
+  static constexpr int kRows = 64;
+  static constexpr int kSlots = D / 8 + 1;                 // 17 (D = 128) or 9 (D = 64)
+  static constexpr int kInsts = kSlots;                    // kRows * kSlots / 64
+  static constexpr int kPerWave = kInsts / kWaves;         // + 1 for one wave
+  static_assert(kInsts % kWaves == 1, "one remainder instruction per unit");
+};
+
+// Per-lane byte offset of unit instruction i (relative to the unit's first row).
+template <int D>
+__device__ __forceinline__ int unit_dma_offset(int i, int64_t st, int lane) {
+  using U = UnitDma<D>;
+  const int slot = 64 * i + lane;
+  const int row = slot / U::kSlots, chunk = slot % U::kSlots;
+  return chunk < D / 8 ? (int)((row * st + chunk * 8) * 2) : 0x7ffffff0;
+}
+
+// Wave `wave`'s share of a unit copy: instructions wave + 4 j, plus the last
+// instruction when wave == extra_wave.  voff[j] = unit_dma_offset(wave + 4 j),
+// voff[kPerWave] = unit_dma_offset(kInsts - 1).
+template <int D>
+__device__ __forceinline__ void unit_dma(__bf16* dst, __amdgpu_buffer_rsrc_t src, const int* voff,
+                                         int wave, int extra_wave) {
+  using U = UnitDma<D>;
+#pragma unroll
+  for (int j = 0; j < U::kPerWave; ++j)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        src, (__attribute__((address_space(3))) void*)(dst + (wave + kWaves * j) * 64 * 8), 16,
+        voff[j], 0, 0, 0);
+  if (wave == extra_wave)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        src, (__attribute__((address_space(3))) void*)(dst + (U::kInsts - 1) * 64 * 8), 16,
+        voff[U::kPerWave], 0, 0, 0);
+}
+
+// Work-group barrier that first drains this wave's outstanding global->LDS
+// copies and LDS accesses (the plain __syncthreads fence would also wait for
+// them, but the explicit form keeps the compiler from hoisting LDS reads
+// across it and documents what the pipeline relies on).
+__device__ __forceinline__ void dma_barrier() {
+  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 // Bit of accumulator entry i in a bitmap word already shifted right by g.
 __device__ __forceinline__ constexpr int acc_tok_bit(int i) {
   return 16 * (i >> 3) + 4 * (i & 3) + 2 * ((i >> 2) & 1);
@@ -122,17 +184,32 @@ __device__ __forceinline__ float halves_sum(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// Sign-extended bit `bit` of x (0 or -1) as one v_bfe_i32; written as inline
+// assembly because the compiler otherwise expands the and-mask of a one-bit
+// field into a compare and a select.
+template <int bit>
+__device__ __forceinline__ int sbfe1_c(uint32_t x) {
+  int r;
+  asm("v_bfe_i32 %0, %1, %2, 1" : "=v"(r) : "v"(x), "i"(bit));
+  return r;
+}
+
 // MFMA accumulator seed for a mixed 32x32 block: 0 where the pair is allowed,
-// -inf where it is masked.  `sw` is the lane's bitmap word (bit t = token t
-// of the block) shifted right by the lane group g.
-__device__ __forceinline__ f32x16 mask_bias(uint32_t sw) {
-  f32x16 c;
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    // bit set -> keep = 0 -> +0.0; bit clear -> keep = ~0 -> 0xff800000 = -inf
-    const uint32_t keep = ((sw >> acc_tok_bit(i)) & 1u) - 1u;
-    c[i] = __uint_as_float(keep & 0xff800000u);
+// -inf where it is masked.  `nw` is the complement of the lane's bitmap word
+// (bit t = token t of the block) shifted right by the lane group g, so a set
+// bit marks a masked pair: its sign-extended bit field is all ones, which
+// masks in the -inf pattern.
+template <int I = 0>
+__device__ __forceinline__ void mask_bias_fill(f32x16& c, uint32_t nw) {
+  if constexpr (I < 16) {
+    c[I] = __int_as_float(sbfe1_c<acc_tok_bit(I)>(nw) & (int)0xff800000);
+    mask_bias_fill<I + 1>(c, nw);
   }
+}
+
+__device__ __forceinline__ f32x16 mask_bias(uint32_t nw) {
+  f32x16 c;
+  mask_bias_fill(c, nw);
   return c;
 }
 
