@@ -56,6 +56,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(FwdParams p)
   constexpr int kUnit = U::kRows * pitch<D>();
   __shared__ __bf16 k_lo[kUnit], k_hi[kUnit], v_lo[kUnit], v_hi[kUnit];
   __shared__ uint32_t bits_lds[2][kTile * 4];
+  __shared__ uint4 dma_scratch[64];  // sink of the copies no wave owns
 
   const int h = blockIdx.x, b = blockIdx.z;
   const int tid = threadIdx.x, wave = uniform(tid >> 6), lane = tid & 63;
@@ -109,15 +110,22 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(FwdParams p)
   int tiles_v = load_chunk(0);
   auto tile_of = [&](int it) { return __builtin_amdgcn_readlane(tiles_v, it & 63); };
   // K and V rows [t0, t0 + 64) into one half's units.
+  // (t0 >= T, e.g. past the last tile, copies zeros.)
+  const auto krs = slice_rsrc(kbase, p.k_st, T, D);
+  const auto vrs = slice_rsrc(vbase, p.v_st, T, D);
+  const int k_row2 = (int)p.k_st * 2, v_row2 = (int)p.v_st * 2;
   auto load_half = [&](__bf16* kd, __bf16* vd, int t0) {
-    unit_dma<D>(kd, rows_rsrc(kbase, p.k_st, t0, T, D), koff, wave, 0);
-    unit_dma<D>(vd, rows_rsrc(vbase, p.v_st, t0, T, D), voff, wave, 1);
+    unit_dma<D>(kd, krs, koff, t0 * k_row2, wave, 0, dma_scratch);
+    unit_dma<D>(vd, vrs, voff, t0 * v_row2, wave, 1, dma_scratch);
   };
   // Row-major half (128 queries x 4 words) of tile `it`'s bitmap slot; each
   // wave copies 1 KiB (waves w and w + 2 copy the same bytes).
+  // (Tiles without a bitmap, it >= npart, copy zeros.)
   auto load_bits = [&](int it) {
+    const bool has = it < npart;
     const auto rs = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint32_t*>(bits_row + (size_t)it * kTileBitsWords), 0, kTile * 16, 0x00020000);
+        const_cast<uint32_t*>(bits_row + (has ? (size_t)it * kTileBitsWords : 0)), 0,
+        has ? kTile * 16 : 0, 0x00020000);
     __builtin_amdgcn_raw_ptr_buffer_load_lds(
         rs, (__attribute__((address_space(3))) void*)(&bits_lds[it & 1][(wave & 1) * 256]), 16,
         (wave & 1) * 1024 + lane * 16, 0, 0, 0);
@@ -130,37 +138,41 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(FwdParams p)
 
   // One 64-key half: S^T = K Q^T (+ mask seed), lazy-rescaled online softmax,
   // O^T += V^T P^T.  w0, w1: bitmap words of the half's two 32-key blocks.
+  // A half with any allowed pair is computed whole (a block without one gets
+  // an all -inf seed), which keeps each contraction one straight-line run of
+  // two interleaved accumulator chains.
   auto half_step = [&](const __bf16* kt_lds, const __bf16* vt_lds, uint32_t w0, uint32_t w1,
                        bool partial) {
-    const uint32_t w2[2] = {w0, w1};
-    bool act[2], mixed[2];
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      act[j] = !partial || __ballot(w2[j] != 0u) != 0ull;
-      mixed[j] = partial && __ballot(w2[j] != ~0u) != 0ull;
-    }
-    if (!act[0] && !act[1]) return;
+    if (partial && __ballot((w0 | w1) != 0u) == 0ull) return;
     f32x16 st[2];
+    if (partial && __ballot((w0 & w1) != ~0u) != 0ull) {
+      st[0] = mask_bias(~(w0 >> g));
+      st[1] = mask_bias(~(w1 >> g));
+    } else {
+      st[0] = f32x16{};
+      st[1] = f32x16{};
+    }
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      if (!act[j]) continue;
-      const bf16x8 kf0 = lds_row8<D>(kt_lds, 32 * j + tok_perm(n), 8 * g);
-      if (mixed[j]) st[j] = mfma32(kf0, qf[0], mask_bias(~(w2[j] >> g)));
-      else st[j] = mfma32(kf0, qf[0], f32x16{});
+    for (int s = 0; s < KS; ++s)
 #pragma unroll
-      for (int s = 1; s < KS; ++s) {
+      for (int j = 0; j < 2; ++j) {
         const bf16x8 kf = lds_row8<D>(kt_lds, 32 * j + tok_perm(n), 16 * s + 8 * g);
         st[j] = mfma32(kf, qf[s], st[j]);
       }
+    // Issue the K reads a few MFMAs ahead of their use.
+    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+    for (int i = 0; i < 2 * KS - 4; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
     }
+    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
 
     float mx = -INFINITY;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      if (!act[j]) continue;
+    for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int i = 0; i < 16; ++i) mx = fmaxf(mx, st[j][i]);
-    }
     mx = halves_max(mx);
     // The reference moves only when the row max exceeds it by 8 (log2
     // units); -inf - -inf compares false, so untouched rows never move.
@@ -174,30 +186,33 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(FwdParams p)
     }
     const float neg = m_ref == -INFINITY ? 0.f : -m_ref * c;
     float rs = 0.f;
+    bf16x8 pf[4];
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      if (!act[j]) continue;
+    for (int s = 0; s < 4; ++s)  // k-step s: entries [8 (s & 1), + 8) of block s >> 1
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const float e = fast_exp2(fmaf(st[j][i], c, neg));
-        st[j][i] = e;
+      for (int k = 0; k < 8; ++k) {
+        const float e = fast_exp2(fmaf(st[s >> 1][8 * (s & 1) + k], c, neg));
+        pf[s][k] = (__bf16)e;
         rs += e;
       }
-    }
     l_run += halves_sum(rs);
 
     // O^T += V^T P^T, 16 keys per k-step.
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const int j = s >> 1, hh = s & 1;
-      if (!act[j]) continue;
-      const bf16x8 pf = pack_half(st[j], hh);
+    for (int s = 0; s < 4; ++s)
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) {
-        const bf16x8 vf = lds_col8<D>(vt_lds, 32 * j + 16 * hh, 32 * dt, lane);
-        oacc[dt] = mfma32(vf, pf, oacc[dt]);
+        const bf16x8 vf = lds_col8<D>(vt_lds, 16 * s, 32 * dt, lane);
+        oacc[dt] = mfma32(vf, pf[s], oacc[dt]);
       }
+    // V transpose reads one k-step (DT MFMAs) ahead.
+    __builtin_amdgcn_sched_group_barrier(0x100, 2 * DT, 1);
+#pragma unroll
+    for (int i = 0; i < 3 * DT; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);
     }
+    __builtin_amdgcn_sched_group_barrier(0x008, DT, 1);
   };
 
   int k0_next = ntiles > 0 ? tile_of(0) * kTile : 0;
@@ -211,18 +226,21 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(FwdParams p)
     // Keys [k0, k0 + 64): its units and bitmap have landed; the other half's
     // units are free again.
     dma_barrier();
-    load_half(k_hi, v_hi, k0 + 64);
     uint4 mbits = make_uint4(~0u, ~0u, ~0u, ~0u);
     if (partial) mbits = *reinterpret_cast<const uint4*>(&bits_lds[it & 1][qloc * 4]);
+    load_half(k_hi, v_hi, k0 + 64);
     half_step(k_lo, v_lo, mbits.x, mbits.y, partial);
 
     // Keys [k0 + 64, k0 + 128); the first half's units are free again.
     dma_barrier();
-    if (it + 1 < ntiles) {
+    const bool more = it + 1 < ntiles;
+    if (more) {
       if (((it + 1) & 63) == 0) tiles_v = load_chunk((it + 1) >> 6);
       k0_next = tile_of(it + 1) * kTile;
+    }
+    if (more) {
       load_half(k_lo, v_lo, k0_next);
-      if (it + 1 < npart) load_bits(it + 1);
+      load_bits(it + 1);
     }
     half_step(k_hi, v_hi, mbits.z, mbits.w, partial);
   }

@@ -23,10 +23,17 @@ int hip_status(hipError_t e, const char* what) {
   return fail(T2T_EHIP, "%s: %s", what, hipGetErrorString(e));
 }
 
-bool view_ok(const t2t_tensor* t) {
-  return t && t->data && t->stride_b >= 0 && t->stride_h >= 0 && t->stride_t > 0 &&
-         (reinterpret_cast<uintptr_t>(t->data) % 16) == 0 && (t->stride_t % 8) == 0 &&
-         (t->stride_h % 8) == 0 && (t->stride_b % 8) == 0;
+// A [B, H, T, D] view the kernels can address: 16-byte aligned rows, and each
+// [T, D] slice, extended by one 128-row tile, spans less than 2 GiB, since the
+// kernels address a slice through a buffer resource with 31-bit byte offsets
+// (a tile starting at or past T is addressed, and reads as zeros).
+bool view_ok(const t2t_tensor* t, int T, int D) {
+  if (!(t && t->data && t->stride_b >= 0 && t->stride_h >= 0 && t->stride_t > 0 &&
+        (reinterpret_cast<uintptr_t>(t->data) % 16) == 0 && (t->stride_t % 8) == 0 &&
+        (t->stride_h % 8) == 0 && (t->stride_b % 8) == 0))
+    return false;
+  const int64_t span_bytes = ((int64_t)T + t2t::kTile) * t->stride_t * 2 + (int64_t)D * 2;
+  return span_bytes <= 0x7fffffffLL - 16;
 }
 
 t2t::TensorView as_view(const t2t_tensor* t) {
@@ -123,8 +130,8 @@ int t2t_attn_fwd(const t2t_tensor* q, const t2t_tensor* k, const t2t_tensor* v,
   int rc = check_dims(B, Hq, Hkv, T, D, dtype);
   if (rc) return rc;
   if (B == 0 || Hq == 0 || T == 0) return T2T_OK;
-  if (!view_ok(q) || !view_ok(k) || !view_ok(v) || !view_ok(o))
-    return fail(T2T_EINVAL, "q/k/v/o view invalid (NULL, misaligned or bad stride)");
+  if (!view_ok(q, T, D) || !view_ok(k, T, D) || !view_ok(v, T, D) || !view_ok(o, T, D))
+    return fail(T2T_EINVAL, "q/k/v/o view invalid (NULL, misaligned, bad stride or slice >= 2 GiB)");
   if (!lse2) return fail(T2T_EINVAL, "lse2 is NULL");
   rc = check_mask(mask, B, T, true, false);
   if (rc) return rc;
@@ -141,7 +148,7 @@ int t2t_attn_bwd_preprocess(const t2t_tensor* o, const t2t_tensor* dout, float* 
   int rc = check_dims(B, Hq, Hq > 0 ? Hq : 1, T, D, dtype);
   if (rc) return rc;
   if (B == 0 || Hq == 0 || T == 0) return T2T_OK;
-  if (!view_ok(o) || !view_ok(dout)) return fail(T2T_EINVAL, "o/dout view invalid");
+  if (!view_ok(o, T, D) || !view_ok(dout, T, D)) return fail(T2T_EINVAL, "o/dout view invalid");
   if (!delta) return fail(T2T_EINVAL, "delta is NULL");
   const t2t::TensorView none{nullptr, 0, 0, 0};
   t2t::AttnDims dims{B, Hq, Hq, T, D, 1.f};
@@ -160,9 +167,9 @@ int t2t_attn_bwd_dkdv(const t2t_tensor* q, const t2t_tensor* k, const t2t_tensor
   int rc = check_dims(B, Hq, Hkv, T, D, dtype);
   if (rc) return rc;
   if (B == 0 || Hq == 0 || T == 0) return T2T_OK;
-  if (!view_ok(q) || !view_ok(k) || !view_ok(v) || !view_ok(dout) || !view_ok(dk) ||
-      !view_ok(dv))
-    return fail(T2T_EINVAL, "tensor view invalid (NULL, misaligned or bad stride)");
+  if (!view_ok(q, T, D) || !view_ok(k, T, D) || !view_ok(v, T, D) || !view_ok(dout, T, D) || !view_ok(dk, T, D) ||
+      !view_ok(dv, T, D))
+    return fail(T2T_EINVAL, "tensor view invalid (NULL, misaligned, bad stride or slice >= 2 GiB)");
   if (!lse2 || !delta) return fail(T2T_EINVAL, "lse2/delta is NULL");
   rc = check_mask(mask, B, T, false, true);
   if (rc) return rc;
@@ -183,8 +190,8 @@ int t2t_attn_bwd_dq(const t2t_tensor* q, const t2t_tensor* k, const t2t_tensor* 
   int rc = check_dims(B, Hq, Hkv, T, D, dtype);
   if (rc) return rc;
   if (B == 0 || Hq == 0 || T == 0) return T2T_OK;
-  if (!view_ok(q) || !view_ok(k) || !view_ok(v) || !view_ok(dout) || !view_ok(dq))
-    return fail(T2T_EINVAL, "tensor view invalid (NULL, misaligned or bad stride)");
+  if (!view_ok(q, T, D) || !view_ok(k, T, D) || !view_ok(v, T, D) || !view_ok(dout, T, D) || !view_ok(dq, T, D))
+    return fail(T2T_EINVAL, "tensor view invalid (NULL, misaligned, bad stride or slice >= 2 GiB)");
   if (!lse2 || !delta) return fail(T2T_EINVAL, "lse2/delta is NULL");
   rc = check_mask(mask, B, T, true, false);
   if (rc) return rc;
@@ -208,9 +215,9 @@ int t2t_attn_bwd(const t2t_tensor* q, const t2t_tensor* k, const t2t_tensor* v,
   int rc = check_dims(B, Hq, Hkv, T, D, dtype);
   if (rc) return rc;
   if (B == 0 || Hq == 0 || T == 0) return T2T_OK;
-  if (!view_ok(q) || !view_ok(k) || !view_ok(v) || !view_ok(o) || !view_ok(dout) ||
-      !view_ok(dq) || !view_ok(dk) || !view_ok(dv))
-    return fail(T2T_EINVAL, "tensor view invalid (NULL, misaligned or bad stride)");
+  if (!view_ok(q, T, D) || !view_ok(k, T, D) || !view_ok(v, T, D) || !view_ok(o, T, D) || !view_ok(dout, T, D) ||
+      !view_ok(dq, T, D) || !view_ok(dk, T, D) || !view_ok(dv, T, D))
+    return fail(T2T_EINVAL, "tensor view invalid (NULL, misaligned, bad stride or slice >= 2 GiB)");
   if (!lse2 || !delta) return fail(T2T_EINVAL, "lse2/delta is NULL");
   rc = check_mask(mask, B, T, true, true);
   if (rc) return rc;

@@ -62,18 +62,6 @@ __device__ __forceinline__ constexpr int acc_tok(int i, int g) {
   return 16 * (i >> 3) + 4 * (i & 3) + 2 * ((i >> 2) & 1) + g;
 }
 
-// Buffer resource over rows [t0, T) of a [T, D] slice (row stride `st`
-// elements).  The range check of a raw buffer load covers the per-lane
-// offset, so rows at or past T read as zeros whatever the tile position.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_rsrc(const __bf16* base, int64_t st,
-                                                             int t0, int T, int D) {
-  const int64_t rows = (int64_t)T - t0;
-  const int64_t bytes = rows > 0 ? ((rows - 1) * st + D) * 2 : 0;
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<__bf16*>(base + (rows > 0 ? (int64_t)t0 * st : 0)), 0,
-                                           (int)(bytes < 0x7fffffff ? bytes : 0x7fffffff),
-                                           0x00020000);
-}
-
 // Direct global -> LDS copies (buffer_load ... lds, no staging registers) of
 // 64 token rows into a padded LDS unit [64][D + 8].  One instruction moves 64
 // lanes x 16 bytes into 64 consecutive 16-byte LDS slots; a padded row is
@@ -98,22 +86,29 @@ __device__ __forceinline__ int unit_dma_offset(int i, int64_t st, int lane) {
   return chunk < D / 8 ? (int)((row * st + chunk * 8) * 2) : 0x7ffffff0;
 }
 
-// Wave `wave`'s share of a unit copy: instructions wave + 4 j, plus the last
-// instruction when wave == extra_wave.  voff[j] = unit_dma_offset(wave + 4 j),
+// Wave `wave`'s share of a unit copy: instructions wave + 4 j, plus the
+// unit's last instruction, which every wave issues so that the sequence has
+// no branch: wave `extra_wave` copies it into the unit, the other waves send
+// an out-of-range load (zeros, no memory touched) into `scratch` (1 KiB of
+// LDS nobody reads).  voff[j] = unit_dma_offset(wave + 4 j),
 // voff[kPerWave] = unit_dma_offset(kInsts - 1).
+// `src` covers the whole [T, D] slice (slice_rsrc) and `row_off` is the byte
+// offset of the unit's first row; it is added to the per-lane offset, whose
+// range check then zero-fills rows at or past T (the host keeps every such
+// offset below 2^31).
 template <int D>
 __device__ __forceinline__ void unit_dma(__bf16* dst, __amdgpu_buffer_rsrc_t src, const int* voff,
-                                         int wave, int extra_wave) {
+                                         int row_off, int wave, int extra_wave, void* scratch) {
   using U = UnitDma<D>;
 #pragma unroll
   for (int j = 0; j < U::kPerWave; ++j)
     __builtin_amdgcn_raw_ptr_buffer_load_lds(
         src, (__attribute__((address_space(3))) void*)(dst + (wave + kWaves * j) * 64 * 8), 16,
-        voff[j], 0, 0, 0);
-  if (wave == extra_wave)
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(
-        src, (__attribute__((address_space(3))) void*)(dst + (U::kInsts - 1) * 64 * 8), 16,
-        voff[U::kPerWave], 0, 0, 0);
+        voff[j] + row_off, 0, 0, 0);
+  const bool mine = wave == extra_wave;
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(
+      src, (__attribute__((address_space(3))) void*)(mine ? (void*)(dst + (U::kInsts - 1) * 64 * 8) : scratch),
+      16, mine ? voff[U::kPerWave] + row_off : 0x7ffffff0, 0, 0, 0);
 }
 
 // Work-group barrier that first drains this wave's outstanding global->LDS
