@@ -77,36 +77,38 @@ __global__ __launch_bounds__(kThreads) void bwd_delta_kernel(BwdParams p) {
   if (rowid < nrows && sub == 0) p.delta[rowid] = acc;
 }
 
-constexpr int kDkdvThreads = 512;  // 8 waves: 4 key groups x 2 query halves
-
-template <int D>
-struct DkdvSmem {
-  __bf16 k[kTile * pitch<D>()];       // this work-group's keys / values
-  __bf16 v[kTile * pitch<D>()];
-  union {
-    struct {
-      __bf16 q[kTile * pitch<D>()];   // current query tile
-      __bf16 dout[kTile * pitch<D>()];
-      float lse2[kTile];              // per query, in accumulator-row order
-      float delta[kTile];
-    } t;
-    float red[4][D / 32][16][64];  // partial dK or dV of the second query half
-  };
-};
+constexpr int kDkdvWaves = 8;  // 4 key groups x 2 query blocks
+constexpr int kDkdvThreads = 64 * kDkdvWaves;
 
 // dK, dV for one (b, kv head, 128-key tile).  8 waves: wave (kw, qh) owns
-// keys 32 kw .. 32 kw + 31 and queries 64 qh .. 64 qh + 63 of every query
-// tile; the two query halves are summed through LDS at the end.  S = Q K^T and
-// dP = dO V^T put the key in the lane and the query in the accumulator rows,
-// so P and dS feed dV^T += dO^T P and dK^T += Q^T dS directly as B operands.
+// keys 32 kw .. 32 kw + 31.  Each query tile is consumed as two 64-query
+// halves; in the phase of a half, wave (kw, qh) takes its queries
+// 32 qh .. 32 qh + 31, and the two query blocks of a key group are summed
+// through LDS at the end.  S = Q K^T and dP = dO V^T put the key in the lane
+// and the query in the accumulator rows, so P and dS feed dV^T += dO^T P and
+// dK^T += Q^T dS directly as B operands.
+//
+// K and V stay in LDS for the whole column.  Q, dO, LSE and Delta stream
+// through LDS per 64-query half: while the waves compute on one half, the
+// other half's units are refilled by direct global->LDS copies issued right
+// after the barrier that retired them (the next (head, tile) item's first
+// half is fetched during the current item's second half), so each copy has
+// one phase of compute to land in.
 template <int D>
 __global__ __launch_bounds__(kDkdvThreads, 1) void bwd_dkdv_kernel(BwdParams p) {
   constexpr int KS = D / 16;
   constexpr int DT = D / 32;
-  __shared__ DkdvSmem<D> sm;
+  using U = UnitDma<D, kDkdvWaves>;
+  constexpr int kUnit = U::kRows * pitch<D>();
+  __shared__ __bf16 k_s[kTile * pitch<D>()], v_s[kTile * pitch<D>()];
+  __shared__ __bf16 q_lo[kUnit], q_hi[kUnit], do_lo[kUnit], do_hi[kUnit];
+  // LSE (log2 domain) and Delta of a half, slot 32 blk + m = query
+  // 32 blk + tok_perm(m) (accumulator-row order).
+  __shared__ float lse_lo[64], lse_hi[64], dl_lo[64], dl_hi[64];
+  __shared__ uint4 dma_scratch[64];
 
   const int hk = blockIdx.x, b = blockIdx.z;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x, wave = uniform(tid >> 6), lane = tid & 63;
   const int kw = wave & 3, qh = wave >> 2;
   const int g = lane >> 5, n = lane & 31;
   const int G = p.Hq / p.Hkv;
@@ -120,124 +122,185 @@ __global__ __launch_bounds__(kDkdvThreads, 1) void bwd_dkdv_kernel(BwdParams p) 
   const float c = p.scale_log2;
 
   // K and V of the key tile stay in LDS; lane (g, n) reads row kloc as the B
-  // operand (k = d, n = key) of S = Q K^T and dP = dO V^T.
-  load_tile_lds<D, kDkdvThreads>(sm.k, slice_rsrc(p.k + b * p.k_sb + hk * p.k_sh, p.k_st, T, D),
+  // operand (k = d, n = key) of S = Q K^T and dP = dO V^T.  (The first
+  // barrier of the loop publishes them.)
+  load_tile_lds<D, kDkdvThreads>(k_s, slice_rsrc(p.k + b * p.k_sb + hk * p.k_sh, p.k_st, T, D),
                                  p.k_st, k0, tid);
-  load_tile_lds<D, kDkdvThreads>(sm.v, slice_rsrc(p.v + b * p.v_sb + hk * p.v_sh, p.v_st, T, D),
+  load_tile_lds<D, kDkdvThreads>(v_s, slice_rsrc(p.v + b * p.v_sb + hk * p.v_sh, p.v_st, T, D),
                                  p.v_st, k0, tid);
 
   const size_t col = (size_t)mb * nt + kt;
   const int npart = uniform(p.m.q_num[col]);
   const int nfull = uniform(p.m.full_q_num[col]);
+  const int nq = npart + nfull;
+  const int nu = G * nq;  // (query head, query tile) items
   const int32_t* pidx = p.m.q_idx + col * nt;
   const int32_t* fidx = p.m.full_q_idx + col * nt;
   const int32_t* pslot = p.m.q_bits_slot + col * nt;
   const uint32_t* bits_col = p.m.tile_bits + kTile * 4 + kloc * 4;
 
+  int qoff[U::kPerWave + 1], ooff[U::kPerWave + 1];
+#pragma unroll
+  for (int j = 0; j < U::kPerWave; ++j) {
+    qoff[j] = unit_dma_offset<D>(wave + kDkdvWaves * j, p.q_st, lane);
+    ooff[j] = unit_dma_offset<D>(wave + kDkdvWaves * j, p.do_st, lane);
+  }
+  qoff[U::kPerWave] = unit_dma_offset<D>(U::kInsts - 1, p.q_st, lane);
+  ooff[U::kPerWave] = unit_dma_offset<D>(U::kInsts - 1, p.do_st, lane);
+  const int lrow = 32 * (lane >> 5) + tok_perm(lane & 31);  // query of LSE / Delta slot `lane`
+
+  // Query-tile list of the column, 64 entries per chunk (lane j: entry
+  // 64 * chunk + j), read back with readlane; reloaded when a chunk changes.
+  int chunk = 0;
+  auto load_chunk = [&](int ch) {
+    const int it = 64 * ch + lane;
+    return make_int2(it < npart ? pidx[it] : (it < nq ? fidx[it - npart] : 0),
+                     it < npart ? pslot[it] : 0);
+  };
+  int2 list_v = load_chunk(0);
+  auto entry = [&](int it) {
+    if ((it >> 6) != chunk) {
+      chunk = it >> 6;
+      list_v = load_chunk(chunk);
+    }
+    return make_int2(__builtin_amdgcn_readlane(list_v.x, it & 63),
+                     __builtin_amdgcn_readlane(list_v.y, it & 63));
+  };
+
+  // Copies of query rows [r0, r0 + 64) of head h into one half's units
+  // (Q + LSE, dO + Delta).  LSE and Delta go one dword per lane, gathered
+  // into accumulator-row order; rows at or past T read zero.
+  auto load_q_part = [&](__bf16* qd, float* ld, int h, int r0) {
+    const auto qrs = slice_rsrc(p.q + b * p.q_sb + h * p.q_sh, p.q_st, T, D);
+    unit_dma<D, kDkdvWaves>(qd, qrs, qoff, r0 * (int)p.q_st * 2, wave, 0, dma_scratch);
+    const auto lrs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(p.lse2 + ((size_t)b * p.Hq + h) * T), 0, T * 4, 0x00020000);
+    if (wave == 2)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(lrs, (__attribute__((address_space(3))) void*)ld, 4,
+                                               (r0 + lrow) * 4, 0, 0, 0);
+  };
+  auto load_do_part = [&](__bf16* dd, float* dld, int h, int r0) {
+    const auto drs = slice_rsrc(p.dout + b * p.do_sb + h * p.do_sh, p.do_st, T, D);
+    unit_dma<D, kDkdvWaves>(dd, drs, ooff, r0 * (int)p.do_st * 2, wave, 1, dma_scratch);
+    const auto drs2 = __builtin_amdgcn_make_buffer_rsrc(p.delta + ((size_t)b * p.Hq + h) * T, 0,
+                                                        T * 4, 0x00020000);
+    if (wave == 3)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(drs2, (__attribute__((address_space(3))) void*)dld,
+                                               4, (r0 + lrow) * 4, 0, 0, 0);
+  };
+  // The lane's bitmap words (its key, queries 32 w .. 32 w + 31, w = 0..3)
+  // of a partial tile; full tiles carry all ones.
+  auto tile_words = [&](int2 e, bool partial) {
+    uint4 w = make_uint4(~0u, ~0u, ~0u, ~0u);
+    if (partial) w = *reinterpret_cast<const uint4*>(bits_col + (size_t)e.y * kTileBitsWords);
+    return w;
+  };
+
   f32x16 dkacc[DT], dvacc[DT];
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) { dkacc[dt] = f32x16{}; dvacc[dt] = f32x16{}; }
 
-  for (int hh = 0; hh < G; ++hh) {
-    const int h = hk * G + hh;
-    const auto qrs = slice_rsrc(p.q + b * p.q_sb + h * p.q_sh, p.q_st, T, D);
-    const auto dors = slice_rsrc(p.dout + b * p.do_sb + h * p.do_sh, p.do_st, T, D);
-    const float* lrow = p.lse2 + ((size_t)b * p.Hq + h) * T;
-    const float* drow = p.delta + ((size_t)b * p.Hq + h) * T;
-    for (int it = 0; it < npart + nfull; ++it) {
-      const bool partial = it < npart;
-      const int qt = uniform(partial ? pidx[it] : fidx[it - npart]);
-      const int q0 = qt * kTile;
-      uint2 mbits = make_uint2(~0u, ~0u);
-      if (partial)
-        mbits = *reinterpret_cast<const uint2*>(bits_col + (size_t)uniform(pslot[it]) * kTileBitsWords + 2 * qh);
-      __syncthreads();
-      load_tile_lds<D, kDkdvThreads>(sm.t.q, qrs, p.q_st, q0, tid);
-      load_tile_lds<D, kDkdvThreads>(sm.t.dout, dors, p.do_st, q0, tid);
-      if (tid < kTile) {
-        // slot 32 qs + m holds query 32 qs + tok_perm(m) (accumulator-row order)
-        const int t = q0 + (tid & ~31) + tok_perm(tid & 31);
-        const float l = t < T ? lrow[t] : -INFINITY;
-        // Fully masked rows (LSE = -inf) carry P = 0: park them at +inf so
-        // exp2(s * c - lse) vanishes.
-        sm.t.lse2[tid] = (l == -INFINITY) ? INFINITY : l;
-        sm.t.delta[tid] = t < T ? drow[t] : 0.f;
-      }
-      __syncthreads();
-      const uint32_t w2[2] = {mbits.x, mbits.y};
-
+  // One 32-query x 32-key block: rows 32 qh .. 32 qh + 31 of a half's units.
+  auto block = [&](const __bf16* qu, const __bf16* du, const float* lu, const float* dlu,
+                   uint32_t w, bool partial) {
+    if (partial && __ballot(w != 0u) == 0ull) return;
+    const bool mixed = partial && __ballot(w != ~0u) != 0ull;
+    const int rb = 32 * qh;
+    f32x16 sacc = mixed ? mask_bias(~(w >> g)) : f32x16{};
+    f32x16 dpacc = f32x16{};
 #pragma unroll
-      for (int qq = 0; qq < 2; ++qq) {
-        const int qs = 2 * qh + qq;
-        // 32 queries x this wave's 32 keys: empty blocks are skipped, mixed
-        // blocks are masked through the accumulator seed (full tiles carry
-        // all-ones words).
-        if (__ballot(w2[qq] != 0u) == 0ull) continue;
-        const bool mixed = __ballot(w2[qq] != ~0u) != 0ull;
-        f32x16 sacc, dpacc;
-        {
-          const bf16x8 qa = lds_row8<D>(sm.t.q, 32 * qs + tok_perm(n), 8 * g);
-          const bf16x8 da = lds_row8<D>(sm.t.dout, 32 * qs + tok_perm(n), 8 * g);
-          const bf16x8 kb = lds_row8<D>(sm.k, kloc, 8 * g);
-          const bf16x8 vb = lds_row8<D>(sm.v, kloc, 8 * g);
-          if (mixed) sacc = mfma32(qa, kb, mask_bias(~(w2[qq] >> g)));
-          else sacc = mfma32(qa, kb, f32x16{});
-          dpacc = mfma32(da, vb, f32x16{});
-        }
+    for (int s = 0; s < KS; ++s) {
+      const bf16x8 qa = lds_row8<D>(qu, rb + tok_perm(n), 16 * s + 8 * g);
+      const bf16x8 da = lds_row8<D>(du, rb + tok_perm(n), 16 * s + 8 * g);
+      const bf16x8 kb = lds_row8<D>(k_s, kloc, 16 * s + 8 * g);
+      const bf16x8 vb = lds_row8<D>(v_s, kloc, 16 * s + 8 * g);
+      sacc = mfma32(qa, kb, sacc);
+      dpacc = mfma32(da, vb, dpacc);
+    }
 #pragma unroll
-        for (int s = 1; s < KS; ++s) {
-          const bf16x8 qa = lds_row8<D>(sm.t.q, 32 * qs + tok_perm(n), 16 * s + 8 * g);
-          const bf16x8 da = lds_row8<D>(sm.t.dout, 32 * qs + tok_perm(n), 16 * s + 8 * g);
-          const bf16x8 kb = lds_row8<D>(sm.k, kloc, 16 * s + 8 * g);
-          const bf16x8 vb = lds_row8<D>(sm.v, kloc, 16 * s + 8 * g);
-          sacc = mfma32(qa, kb, sacc);
-          dpacc = mfma32(da, vb, dpacc);
-        }
+    for (int i = 0; i < 16; ++i) {
+      const int qr = rb + acc_row(i, g);
+      // A fully masked row has LSE = -inf and only -inf scores; clamping
+      // keeps exp2(-inf - lse) at 0 instead of NaN.
+      const float lse = fmaxf(lu[qr], -3.402823466e38f);
+      const float pv = fast_exp2(fmaf(sacc[i], c, -lse));
+      sacc[i] = pv;                                 // P
+      dpacc[i] = pv * (dpacc[i] - dlu[qr]);         // dS
+    }
+    // dV^T += dO^T P, dK^T += Q^T dS (contraction over the 32 queries).
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int qr = 32 * qs + acc_row(i, g);
-          const float pv = fast_exp2(fmaf(sacc[i], c, -sm.t.lse2[qr]));
-          sacc[i] = pv;                                    // P
-          dpacc[i] = pv * (dpacc[i] - sm.t.delta[qr]);     // dS
-        }
-        // dV^T += dO^T P, dK^T += Q^T dS (contraction over the 32 queries).
+    for (int h2 = 0; h2 < 2; ++h2) {
+      const bf16x8 pb = pack_half(sacc, h2);
+      const bf16x8 sb = pack_half(dpacc, h2);
 #pragma unroll
-        for (int h2 = 0; h2 < 2; ++h2) {
-          const bf16x8 pb = pack_half(sacc, h2);
-          const bf16x8 sb = pack_half(dpacc, h2);
-#pragma unroll
-          for (int dt = 0; dt < DT; ++dt) {
-            const bf16x8 doa = lds_col8<D>(sm.t.dout, 32 * qs + 16 * h2, 32 * dt, lane);
-            const bf16x8 qa = lds_col8<D>(sm.t.q, 32 * qs + 16 * h2, 32 * dt, lane);
-            dvacc[dt] = mfma32(doa, pb, dvacc[dt]);
-            dkacc[dt] = mfma32(qa, sb, dkacc[dt]);
-          }
-        }
+      for (int dt = 0; dt < DT; ++dt) {
+        const bf16x8 doa = lds_col8<D>(du, rb + 16 * h2, 32 * dt, lane);
+        const bf16x8 qa = lds_col8<D>(qu, rb + 16 * h2, 32 * dt, lane);
+        dvacc[dt] = mfma32(doa, pb, dvacc[dt]);
+        dkacc[dt] = mfma32(qa, sb, dkacc[dt]);
       }
     }
+  };
+
+  int2 e_next = make_int2(0, 0);
+  uint4 wb = make_uint4(~0u, ~0u, ~0u, ~0u);
+  if (nu > 0) {
+    e_next = entry(0);
+    load_q_part(q_lo, lse_lo, hk * G, e_next.x * kTile);
+    load_do_part(do_lo, dl_lo, hk * G, e_next.x * kTile);
+    wb = tile_words(e_next, 0 < npart);
+  }
+  for (int u = 0, hh = 0, it = 0; u < nu; ++u) {
+    const int h = hk * G + hh;
+    const int q0 = e_next.x * kTile;
+    const bool partial = it < npart;
+    // Query rows [q0, q0 + 64): their units have landed; the other half's
+    // units are free again.
+    dma_barrier();
+    load_q_part(q_hi, lse_hi, h, q0 + 64);
+    load_do_part(do_hi, dl_hi, h, q0 + 64);
+    block(q_lo, do_lo, lse_lo, dl_lo, qh ? wb.y : wb.x, partial);
+
+    // Query rows [q0 + 64, q0 + 128); the first half's units are free again.
+    dma_barrier();
+    if (++it == nq) { it = 0; ++hh; }
+    uint4 wn = wb;
+    const bool more = u + 1 < nu;
+    const int hn = hk * G + hh;
+    if (more) {
+      e_next = entry(it);
+      load_q_part(q_lo, lse_lo, hn, e_next.x * kTile);
+      load_do_part(do_lo, dl_lo, hn, e_next.x * kTile);
+      wn = tile_words(e_next, it < npart);
+    }
+    block(q_hi, do_hi, lse_hi, dl_hi, qh ? wb.w : wb.z, partial);
+    wb = wn;
   }
 
-  // Sum the two query halves (qh = 1 hands its partials to qh = 0), dK then dV.
-  __syncthreads();
+  // Sum the two query blocks of each key group (qh = 1 hands its partials to
+  // qh = 0 through one of the Q / dO units, 16 KiB per wave), dK then dV.
+  float* red = reinterpret_cast<float*>(kw == 0 ? q_lo : kw == 1 ? q_hi : kw == 2 ? do_lo : do_hi);
+  static_assert(DT * 16 * 64 * sizeof(float) <= kUnit * sizeof(__bf16), "reduction fits a unit");
+  dma_barrier();
   if (qh == 1) {
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) sm.red[kw][dt][i][lane] = dkacc[dt][i];
+      for (int i = 0; i < 16; ++i) red[(dt * 16 + i) * 64 + lane] = dkacc[dt][i];
   }
   __syncthreads();
   if (qh == 0) {
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) dkacc[dt][i] += sm.red[kw][dt][i][lane];
+      for (int i = 0; i < 16; ++i) dkacc[dt][i] += red[(dt * 16 + i) * 64 + lane];
   }
   __syncthreads();
   if (qh == 1) {
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) sm.red[kw][dt][i][lane] = dvacc[dt][i];
+      for (int i = 0; i < 16; ++i) red[(dt * 16 + i) * 64 + lane] = dvacc[dt][i];
   }
   __syncthreads();
   if (qh == 0 && kvalid) {
@@ -246,7 +309,7 @@ __global__ __launch_bounds__(kDkdvThreads, 1) void bwd_dkdv_kernel(BwdParams p) 
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
 #pragma unroll
-      for (int i = 0; i < 16; ++i) dvacc[dt][i] += sm.red[kw][dt][i][lane];
+      for (int i = 0; i < 16; ++i) dvacc[dt][i] += red[(dt * 16 + i) * 64 + lane];
       store_acc_t(dkp, dkacc[dt], 32 * dt, g, p.scale);
       store_acc_t(dvp, dvacc[dt], 32 * dt, g, 1.f);
     }

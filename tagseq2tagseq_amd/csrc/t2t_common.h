@@ -68,13 +68,13 @@ __device__ __forceinline__ constexpr int acc_tok(int i, int g) {
 // kSlots = D / 8 + 1 slots (the last one is the pad, loaded from an offset past
 // any buffer so that it reads zero and touches no memory), so a unit is exactly
 // kSlots instructions.  Instruction i, lane l covers slot 64 i + l.
-template <int D>
+template <int D, int NW = kWaves>
 struct UnitDma {
   static constexpr int kRows = 64;
   static constexpr int kSlots = D / 8 + 1;                 // 17 (D = 128) or 9 (D = 64)
   static constexpr int kInsts = kSlots;                    // kRows * kSlots / 64
-  static constexpr int kPerWave = kInsts / kWaves;         // + 1 for one wave
-  static_assert(kInsts % kWaves == 1, "one remainder instruction per unit");
+  static constexpr int kPerWave = kInsts / NW;             // + 1 for one wave
+  static_assert(kInsts % NW == 1, "one remainder instruction per unit");
 };
 
 // Per-lane byte offset of unit instruction i (relative to the unit's first row).
@@ -86,24 +86,24 @@ __device__ __forceinline__ int unit_dma_offset(int i, int64_t st, int lane) {
   return chunk < D / 8 ? (int)((row * st + chunk * 8) * 2) : 0x7ffffff0;
 }
 
-// Wave `wave`'s share of a unit copy: instructions wave + 4 j, plus the
-// unit's last instruction, which every wave issues so that the sequence has
-// no branch: wave `extra_wave` copies it into the unit, the other waves send
-// an out-of-range load (zeros, no memory touched) into `scratch` (1 KiB of
-// LDS nobody reads).  voff[j] = unit_dma_offset(wave + 4 j),
-// voff[kPerWave] = unit_dma_offset(kInsts - 1).
+// Wave `wave`'s share of a unit copy by NW waves: instructions wave + NW j,
+// plus the unit's last instruction, which every wave issues so that the
+// sequence has no branch: wave `extra_wave` copies it into the unit, the
+// other waves send an out-of-range load (zeros, no memory touched) into
+// `scratch` (1 KiB of LDS nobody reads).  voff[j] = unit_dma_offset(wave +
+// NW j), voff[kPerWave] = unit_dma_offset(kInsts - 1).
 // `src` covers the whole [T, D] slice (slice_rsrc) and `row_off` is the byte
 // offset of the unit's first row; it is added to the per-lane offset, whose
 // range check then zero-fills rows at or past T (the host keeps every such
 // offset below 2^31).
-template <int D>
+template <int D, int NW = kWaves>
 __device__ __forceinline__ void unit_dma(__bf16* dst, __amdgpu_buffer_rsrc_t src, const int* voff,
                                          int row_off, int wave, int extra_wave, void* scratch) {
-  using U = UnitDma<D>;
+  using U = UnitDma<D, NW>;
 #pragma unroll
   for (int j = 0; j < U::kPerWave; ++j)
     __builtin_amdgcn_raw_ptr_buffer_load_lds(
-        src, (__attribute__((address_space(3))) void*)(dst + (wave + kWaves * j) * 64 * 8), 16,
+        src, (__attribute__((address_space(3))) void*)(dst + (wave + NW * j) * 64 * 8), 16,
         voff[j] + row_off, 0, 0, 0);
   const bool mine = wave == extra_wave;
   __builtin_amdgcn_raw_ptr_buffer_load_lds(

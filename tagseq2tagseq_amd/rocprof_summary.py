@@ -1,0 +1,145 @@
+"""Text summaries of rocprofv3 runs of bench.py (kernel durations, HBM traffic).
+
+    python -m tagseq2tagseq_amd.rocprof_summary trace  <kt_dir> <bench_json> <config> > kernel_trace.txt
+    python -m tagseq2tagseq_amd.rocprof_summary traffic <fetch_dir> <write_dir> \
+        <copy_fetch_dir> <copy_write_dir> <config> > hbm_traffic.txt
+
+`trace` reads a `rocprofv3 --kernel-trace` database and lists, per kernel,
+the number of dispatches and their mean / median / min / max duration next to
+bench.py's own HIP-event means (the `kernels_ms` of its JSON line).
+
+`traffic` reads the `--pmc FETCH_SIZE` and `--pmc WRITE_SIZE` databases of a
+bench.py run and of `bench.py --copy-calibration` (1 GiB device copies), and
+scales each counter so that the copy reads as its known size.  bench.py's
+roofline `traffic` field reads the resulting file.
+"""
+from __future__ import annotations
+
+import glob
+import json
+import sqlite3
+import statistics
+import sys
+from collections import defaultdict
+from typing import Dict, List
+
+WORKLOADS = {
+    2: "doc_causal B2 H12 T8192 D64 bf16",
+    3: "cross_doc_link B1 H16 T16384 D128 bf16",
+    4: "cross_doc_link GQA B1 Hq16 Hkv4 T32768 D128 bf16",
+}
+
+
+def _short(name: str) -> str:
+    """Kernel name without the template / argument decoration."""
+    base = name.split("(")[0]
+    if "<" in base:
+        base = base.split("<")[0]
+    return base.split("::")[-1].replace("void ", "").strip()
+
+
+def _db(path: str) -> sqlite3.Connection:
+    dbs = glob.glob(f"{path}/**/*.db", recursive=True)
+    if not dbs:
+        raise SystemExit(f"no rocprofv3 database under {path}")
+    return sqlite3.connect(dbs[0])
+
+
+def kernel_durations(path: str) -> Dict[str, List[float]]:
+    """Dispatch durations (us) per t2t kernel of a kernel-trace database."""
+    out: Dict[str, List[float]] = defaultdict(list)
+    for name, dur in _db(path).execute("select name, duration from kernels"):
+        if "t2t::" in name:
+            out[_short(name)].append(dur / 1000.0)
+    return out
+
+
+def counter_means(path: str, counter: str, match: str = "t2t::") -> Dict[str, float]:
+    """Mean per-dispatch value of one counter (summed over its instances)."""
+    per_dispatch: Dict[tuple, float] = defaultdict(float)
+    con = _db(path)
+    rows = con.execute("select kernel_name, dispatch_id, counter_name, value from counters_collection")
+    for kname, disp, cname, val in rows:
+        if cname == counter and match in kname:
+            per_dispatch[(_short(kname), disp)] += val
+    sums: Dict[str, List[float]] = defaultdict(list)
+    for (k, _), v in per_dispatch.items():
+        sums[k].append(v)
+    return {k: sum(v) / len(v) for k, v in sums.items()}
+
+
+def copy_counter(path: str, counter: str) -> float:
+    """Mean per-dispatch counter value of the calibration copy kernel."""
+    vals = counter_means(path, counter, match="copy")
+    if not vals:
+        raise SystemExit(f"no copy kernel with {counter} under {path}")
+    return max(vals.values())
+
+
+def trace(kt_dir: str, bench_json: str, cfg: int) -> str:
+    durs = kernel_durations(kt_dir)
+    with open(bench_json) as f:
+        bench = json.loads(f.read().strip().splitlines()[-1])
+    ev = bench.get("kernels_ms", {})
+    lines = [
+        f"# rocprofv3 kernel trace -- config {cfg} ({WORKLOADS.get(cfg, '?')}), MI355X",
+        "#",
+        "# command (repo root, GPU box):",
+        f"#   rocprofv3 --kernel-trace --stats -d {kt_dir} -o kt -- \\",
+        f"#       python -u bench.py --config {cfg} --no-cpu-baseline --steps 10 --warmup 3",
+        "# durations in microseconds over every dispatch of the run (warm-up, timed steps and",
+        "# bench.py's per-kernel timing loops); bench.py's own HIP-event means for the same",
+        "# build (separate run, no profiler) are listed for comparison.",
+        "",
+        f"{'kernel':28s} {'calls':>6s} {'mean':>8s} {'median':>8s} {'min':>8s} {'max':>8s}   bench.py HIP events",
+    ]
+    for k, v in sorted(durs.items(), key=lambda kv: -statistics.mean(kv[1])):
+        evk = next((ev[e] for e in ev if e.startswith(k)), None)
+        evs = f"{1000 * evk:10.1f}" if evk is not None else "         -"
+        lines.append(f"{k:28s} {len(v):6d} {statistics.mean(v):8.1f} {statistics.median(v):8.1f} "
+                     f"{min(v):8.1f} {max(v):8.1f}   {evs}")
+    lines.append("")
+    lines.append(f"# bench.py line of that run: value {bench.get('value')} {bench.get('unit')}, "
+                 f"ms_per_step {bench.get('ms_per_step')}")
+    return "\n".join(lines) + "\n"
+
+
+def traffic(fetch_dir: str, write_dir: str, cfetch_dir: str, cwrite_dir: str, cfg: int) -> str:
+    copy_kib = 1024.0 * 1024.0  # bench.py --copy-calibration copies 1 GiB
+    ff = copy_kib / copy_counter(cfetch_dir, "FETCH_SIZE")
+    wf = copy_kib / copy_counter(cwrite_dir, "WRITE_SIZE")
+    fetch = counter_means(fetch_dir, "FETCH_SIZE")
+    write = counter_means(write_dir, "WRITE_SIZE")
+    lines = [
+        f"# HBM traffic per launch -- config {cfg} ({WORKLOADS.get(cfg, '?')}), MI355X",
+        "#",
+        "# commands (repo root, GPU box), one counter per pass:",
+        f"#   rocprofv3 --pmc FETCH_SIZE -d {fetch_dir} -o f -- python -u bench.py --config {cfg} --no-cpu-baseline --steps 2 --warmup 1 --reps 2",
+        f"#   rocprofv3 --pmc WRITE_SIZE -d {write_dir} -o w -- python -u bench.py --config {cfg} --no-cpu-baseline --steps 2 --warmup 1 --reps 2",
+        "# calibration: the same counters on bench.py --copy-calibration (1 GiB device copies):",
+        f"#   rocprofv3 --pmc FETCH_SIZE -d {cfetch_dir} -o cf -- python -u bench.py --copy-calibration",
+        f"#   rocprofv3 --pmc WRITE_SIZE -d {cwrite_dir} -o cw -- python -u bench.py --copy-calibration",
+        f"# copy of {copy_kib:.0f} KiB: factors fetch {ff:.4f}, write {wf:.4f}",
+        "# traffic_bytes = (FETCH_SIZE * fetch_factor + WRITE_SIZE * write_factor) * 1024, mean per dispatch",
+        "",
+        f"fetch_factor={ff:.4f}",
+        f"write_factor={wf:.4f}",
+    ]
+    for k in sorted(fetch, key=lambda k: -fetch[k]):
+        w = write.get(k, 0.0)
+        tb = (fetch[k] * ff + w * wf) * 1024
+        lines.append(f"{k}: fetch_kib={fetch[k]:.1f} write_kib={w:.1f} traffic_bytes={tb:.0f}")
+    return "\n".join(lines) + "\n"
+
+
+def main(argv: List[str]) -> None:
+    if len(argv) >= 4 and argv[0] == "trace":
+        sys.stdout.write(trace(argv[1], argv[2], int(argv[3])))
+    elif len(argv) >= 6 and argv[0] == "traffic":
+        sys.stdout.write(traffic(argv[1], argv[2], argv[3], argv[4], int(argv[5])))
+    else:
+        raise SystemExit(__doc__)
+
+
+if __name__ == "__main__":
+    main(sys.argv[1:])
