@@ -208,6 +208,7 @@ __global__ __launch_bounds__(kDkdvThreads, 1) void bwd_dkdv_kernel(BwdParams p) 
     const int rb = 32 * qh;
     f32x16 sacc = mixed ? mask_bias(~(w >> g)) : f32x16{};
     f32x16 dpacc = f32x16{};
+    __builtin_amdgcn_s_setprio(1);  // MFMA runs at raised wave priority
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
       const bf16x8 qa = lds_row8<D>(qu, rb + tok_perm(n), 16 * s + 8 * g);
@@ -217,6 +218,7 @@ __global__ __launch_bounds__(kDkdvThreads, 1) void bwd_dkdv_kernel(BwdParams p) 
       sacc = mfma32(qa, kb, sacc);
       dpacc = mfma32(da, vb, dpacc);
     }
+    __builtin_amdgcn_s_setprio(0);
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       const int qr = rb + acc_row(i, g);
@@ -228,6 +230,7 @@ __global__ __launch_bounds__(kDkdvThreads, 1) void bwd_dkdv_kernel(BwdParams p) 
       dpacc[i] = pv * (dpacc[i] - dlu[qr]);         // dS
     }
     // dV^T += dO^T P, dK^T += Q^T dS (contraction over the 32 queries).
+    __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int h2 = 0; h2 < 2; ++h2) {
       const bf16x8 pb = pack_half(sacc, h2);
@@ -240,6 +243,7 @@ __global__ __launch_bounds__(kDkdvThreads, 1) void bwd_dkdv_kernel(BwdParams p) 
         dkacc[dt] = mfma32(qa, sb, dkacc[dt]);
       }
     }
+    __builtin_amdgcn_s_setprio(0);
   };
 
   int2 e_next = make_int2(0, 0);
@@ -393,6 +397,7 @@ __global__ __launch_bounds__(kThreads, 2) void bwd_dq_kernel(BwdParams p) {
       if (__ballot(w4[j] != 0u) == 0ull) continue;
       const bool mixed = __ballot(w4[j] != ~0u) != 0ull;
       f32x16 sacc, dpacc;
+      __builtin_amdgcn_s_setprio(1);  // MFMA runs at raised wave priority
       {
         const bf16x8 ka = lds_row8<D>(sm.k, 32 * j + tok_perm(n), 8 * g);
         const bf16x8 va = lds_row8<D>(sm.v, 32 * j + tok_perm(n), 8 * g);
@@ -407,12 +412,14 @@ __global__ __launch_bounds__(kThreads, 2) void bwd_dq_kernel(BwdParams p) {
         sacc = mfma32(ka, qf[s], sacc);
         dpacc = mfma32(va, dof[s], dpacc);
       }
+      __builtin_amdgcn_s_setprio(0);
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const float pv = fast_exp2(fmaf(sacc[i], c, neg_lse));
         dpacc[i] = pv * (dpacc[i] - delta);  // dS^T
       }
       // dQ^T += K^T dS^T (contraction over the 32 keys of block j).
+      __builtin_amdgcn_s_setprio(1);
 #pragma unroll
       for (int h2 = 0; h2 < 2; ++h2) {
         const bf16x8 sb = pack_half(dpacc, h2);
@@ -422,6 +429,7 @@ __global__ __launch_bounds__(kThreads, 2) void bwd_dq_kernel(BwdParams p) {
           dqacc[dt] = mfma32(ka, sb, dqacc[dt]);
         }
       }
+      __builtin_amdgcn_s_setprio(0);
     }
   }
 

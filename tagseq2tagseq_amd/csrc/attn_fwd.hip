@@ -152,6 +152,9 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(FwdParams p)
       st[0] = f32x16{};
       st[1] = f32x16{};
     }
+    // MFMA runs issue at raised wave priority, so that the wave sharing the
+    // SIMD fills the gaps with its softmax instead of competing for issue.
+    __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int s = 0; s < KS; ++s)
 #pragma unroll
@@ -168,6 +171,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(FwdParams p)
     }
     __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
 
+    __builtin_amdgcn_s_setprio(0);
     float mx = -INFINITY;
 #pragma unroll
     for (int j = 0; j < 2; ++j)
@@ -198,6 +202,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(FwdParams p)
     l_run += halves_sum(rs);
 
     // O^T += V^T P^T, 16 keys per k-step.
+    __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int s = 0; s < 4; ++s)
 #pragma unroll
@@ -213,6 +218,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(FwdParams p)
       __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);
     }
     __builtin_amdgcn_sched_group_barrier(0x008, DT, 1);
+    __builtin_amdgcn_s_setprio(0);
   };
 
   int k0_next = ntiles > 0 ? tile_of(0) * kTile : 0;
