@@ -2,8 +2,9 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 3]
 
-One step = one pass of the hot path over one batch: the metadata pass
-(tile classification + BlockMask tables from per-token inputs), the forward
+One step = one pass of the hot path over one batch: the per-token mask
+inputs rebuilt from the device-resident span / link lists (t2t_token_inputs),
+the metadata pass (tile classification + BlockMask tables), the forward
 kernel and the three backward launches, with every input already resident in
 HBM.  Prints one JSON line.
 
@@ -36,6 +37,7 @@ sys.path.insert(0, ROOT)
 from tagseq2tagseq_amd import synth  # noqa: E402
 from tagseq2tagseq_amd.attention import BwdPhases, attn_bwd, attn_fwd  # noqa: E402
 from tagseq2tagseq_amd.block_mask import build_block_mask  # noqa: E402
+from tagseq2tagseq_amd.mask_creators import TokenLists  # noqa: E402
 
 METRIC = "masked attn fwd+bwd useful TFLOP/s + % bf16 MFMA peak, cross_doc_link T=16k"
 PEAK_BF16_TFLOPS = 2516.6   # MI355X dense bf16 MFMA: 256 CU x 2.4 GHz x 4096 FLOP/clk
@@ -192,6 +194,7 @@ def main():
     do = torch.randn(B, Hq, T, D, generator=g).to(torch.bfloat16).to(dev)
     scale = 1.0 / math.sqrt(D)
 
+    W = 0 if qb is None else qb.shape[1]
     n_pairs = 0
     for b in range(B):
         bb = b if len(rows_np) > 1 else 0
@@ -199,8 +202,16 @@ def main():
     causal_pairs = B * T * (T + 1) // 2
     useful_flops = 14.0 * D * n_pairs * Hq
 
+    # Span / link lists resident on the device; each step rebuilds the
+    # per-token inputs from them (t2t_token_inputs), then the metadata pass.
+    lists = TokenLists(T, [r.spans for r in rows], dev, words=W,
+                       link_rows=None if W == 0 else [r.link_rows for r in rows])
+    doc_d, qb_d, kb_d = lists.build()
+    assert torch.equal(doc_d, doc) and (qb is None or (torch.equal(qb_d, qb) and torch.equal(kb_d, kb)))
+
     def step():
-        bm = build_block_mask(doc, qb, kb)
+        d_, q_, k_ = lists.build()
+        bm = build_block_mask(d_, q_, k_)
         out, lse2 = attn_fwd(q, k, v, bm, scale)
         return attn_bwd(q, k, v, out, do, lse2, bm, scale)
 
@@ -224,6 +235,7 @@ def main():
     out, lse2 = attn_fwd(q, k, v, bm, scale)
     ph = BwdPhases(q, k, v, out, do, lse2, bm, scale)
     ph.preprocess()
+    t_tok = time_launches(lists.build, args.reps)
     t_meta = time_launches(lambda: build_block_mask(doc, qb, kb), args.reps)
     t_fwd = time_launches(lambda: attn_fwd(q, k, v, bm, scale), args.reps)
     t_pre = time_launches(ph.preprocess, args.reps)
@@ -242,7 +254,6 @@ def main():
 
     nt = (T + 127) // 128
     Bm = doc.shape[0]
-    W = 0 if qb is None else qb.shape[1]
     tc = bm.tile_class
     tiles = {"full": int((tc == 2).sum()), "partial": int((tc == 1).sum()), "skip": int((tc == 0).sum())}
     # metadata pass, algorithmic bytes: per-token reads + every table written once
@@ -250,6 +261,11 @@ def main():
                   + Bm * nt * nt                           # tile classes
                   + 4 * (5 * Bm * nt * nt + 7 * Bm * nt)   # 4 index + q_bits_slot, 4 counts + 3
                   + 4096 * tiles["partial"])               # two 128x128-bit maps per partial tile
+
+    # token-input builder, algorithmic bytes: the span / grant lists read, the
+    # per-token doc ids and grant words written
+    tok_bytes = (lists.lists.numel() * 4 + (0 if lists.links is None else lists.links.numel() * 8)
+                 + Bm * T * 4 + 2 * 8 * W * Bm * T)
 
     result = {
         "metric": METRIC,
@@ -283,6 +299,7 @@ def main():
             "traffic_source": f"profiles/hbm_traffic_config{args.config}.txt",
         },
         "kernels_ms": {
+            "token_inputs_kernel": round(t_tok, 4),
             "mask_meta (4 launches)": round(t_meta, 4),
             "attn_fwd_bf16_kernel": round(t_fwd, 4),
             "bwd_delta_kernel": round(t_pre, 4),
@@ -291,6 +308,8 @@ def main():
         },
         "mask_meta": {"us": round(t_meta * 1e3, 2), "bytes": int(meta_bytes),
                       "GBps": round(meta_bytes / (t_meta * 1e-3) / 1e9, 2)},
+        "token_inputs": {"us": round(t_tok * 1e3, 2), "bytes": int(tok_bytes),
+                         "GBps": round(tok_bytes / (t_tok * 1e-3) / 1e9, 2)},
         "wall_s_timed": round(wall, 3),
     }
 

@@ -97,6 +97,32 @@ const char *t2t_version(void);
 const char *t2t_last_error(void);
 
 /*
+ * Per-token inputs of t2t_mask_meta, built on the device from span and grant
+ * lists.  Replaces the per-span loop of document_ids
+ * (model/graph_traversal/block_mask_creator.py:107-117) and the per-grant
+ * device slice-ORs of CrossDocLinkMaskCreator._build_grant_bitmasks
+ * (model/graph_traversal/cross_doc_mask.py:240-294), and builds the doc x doc
+ * link-bitmask form of the cross_doc_link mask.
+ *   spans   int32[B][max_spans][3] = (start, end, doc_id), n_spans int32[B]:
+ *           span i covers tokens [start, end) clipped to [0, T); later spans
+ *           overwrite earlier ones; tokens no span covers get doc id -1.
+ *   grants  int32[B][max_grants][5] = (bit, q_start, q_end, kv_start, kv_end),
+ *           n_grants int32[B]; both NULL for no grants.  Bit `bit` of word
+ *           bit / 64 is set in q_bits over [q_start, q_end) and in kv_bits over
+ *           [kv_start, kv_end), clipped to [0, T); bits >= 64 * words are ignored.
+ *   links   uint64[B][max_spans][words] or NULL: q_bits[t] |= links[span(t)],
+ *           kv_bits[t] |= bit span(t) (span(t) = index of the span covering t;
+ *           spans past 64 * words set no key bit).
+ * Counts above max_spans / max_grants are clamped.  Outputs doc int32[B][T]
+ * and, when words > 0, q_bits / kv_bits uint64[B][words][T] (the layout
+ * t2t_mask_meta reads).
+ */
+int t2t_token_inputs(const int32_t *spans, const int32_t *n_spans, int32_t max_spans,
+                     const int32_t *grants, const int32_t *n_grants, int32_t max_grants,
+                     const uint64_t *links, int32_t B, int32_t T, int32_t words,
+                     int32_t *doc, uint64_t *q_bits, uint64_t *kv_bits, void *stream);
+
+/*
  * Metadata pass: tile classification, the BlockMask tables and the partial
  * tile bitmaps, written into the buffers `out` points at.
  * Replaces create_block_mask(mask_mod, B=None, H=None, T, T)

@@ -42,6 +42,8 @@ _I32 = ctypes.c_int32
 _SIGS = {
     "t2t_version": ([], ctypes.c_char_p),
     "t2t_last_error": ([], ctypes.c_char_p),
+    "t2t_token_inputs": ([_P, _P, _I32, _P, _P, _I32, _P, _I32, _I32, _I32, _P, _P, _P, _P],
+                         ctypes.c_int),
     "t2t_mask_meta": ([_P, _P, _P, _I32, _I32, _I32, _P, _P, _P], ctypes.c_int),
     "t2t_attn_fwd": ([_P] * 5 + [_I32] * 6 + [ctypes.c_float, _P, _P], ctypes.c_int),
     "t2t_attn_bwd": ([_P] * 10 + [_I32] * 6 + [ctypes.c_float, _P, _P], ctypes.c_int),

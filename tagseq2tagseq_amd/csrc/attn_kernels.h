@@ -57,6 +57,11 @@ struct AttnDims {
 
 constexpr int kTileBitsWords = 2 * kTile * 4;  // uint32 words per tile bitmap slot
 
+hipError_t launch_token_inputs(const int32_t* spans, const int32_t* n_spans, int max_spans,
+                               const int32_t* grants, const int32_t* n_grants, int max_grants,
+                               const uint64_t* links, int B, int T, int words, int32_t* doc,
+                               uint64_t* q_bits, uint64_t* kv_bits, hipStream_t stream);
+
 hipError_t launch_mask_meta(const int32_t* doc, const uint64_t* qbits, const uint64_t* kvbits,
                             int T, int words, const MaskOut& out, hipStream_t stream);
 

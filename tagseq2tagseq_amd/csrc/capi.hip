@@ -88,6 +88,29 @@ const char* t2t_version(void) { return "t2t_attn 0.1 gfx950"; }
 
 const char* t2t_last_error(void) { return g_err; }
 
+int t2t_token_inputs(const int32_t* spans, const int32_t* n_spans, int32_t max_spans,
+                     const int32_t* grants, const int32_t* n_grants, int32_t max_grants,
+                     const uint64_t* links, int32_t B, int32_t T, int32_t words, int32_t* doc,
+                     uint64_t* q_bits, uint64_t* kv_bits, void* stream) {
+  if (B < 0 || T < 0 || max_spans < 0 || max_grants < 0)
+    return fail(T2T_EINVAL, "negative B, T, max_spans or max_grants");
+  if (words < 0 || words > T2T_MAX_WORDS)
+    return fail(T2T_EUNSUPPORTED, "words=%d outside [0, %d]", words, T2T_MAX_WORDS);
+  if (B == 0 || T == 0) return T2T_OK;
+  if (!doc || !n_spans || (max_spans > 0 && !spans))
+    return fail(T2T_EINVAL, "doc, n_spans or spans is NULL");
+  if ((grants == nullptr) != (n_grants == nullptr))
+    return fail(T2T_EINVAL, "grants and n_grants must both be given or both be NULL");
+  if (grants && max_grants == 0) return fail(T2T_EINVAL, "grants given with max_grants == 0");
+  if ((grants || links) && words == 0)
+    return fail(T2T_EINVAL, "grants / links need words > 0");
+  if (words > 0 && (!q_bits || !kv_bits)) return fail(T2T_EINVAL, "q_bits / kv_bits is NULL");
+  return hip_status(t2t::launch_token_inputs(spans, n_spans, max_spans, grants, n_grants,
+                                             max_grants, links, B, T, words, doc, q_bits,
+                                             kv_bits, static_cast<hipStream_t>(stream)),
+                    "t2t_token_inputs launch");
+}
+
 int t2t_mask_meta(const int32_t* doc, const uint64_t* q_bits, const uint64_t* kv_bits,
                   int32_t mask_batch, int32_t T, int32_t words, int8_t* tile_class,
                   const t2t_block_mask* out, void* stream) {

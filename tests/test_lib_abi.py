@@ -104,3 +104,26 @@ def test_flex_attention_validation_on_cpu():
         flex_attention(q, q, q)
     with pytest.raises(NotImplementedError):
         flex_attention(q, q, q, score_mod=lambda s, b, h, i, j: s, block_mask=object())
+
+
+@no_gpu
+def test_token_inputs_argument_checks():
+    lib = _lib.lib()
+    P = ctypes.c_void_p(0x1000)
+    # empty work is a no-op
+    assert lib.t2t_token_inputs(None, None, 0, None, None, 0, None, 0, 16, 0, None, None, None,
+                                None) == 0
+    assert lib.t2t_token_inputs(P, P, 4, None, None, 0, None, 1, -1, 0, P, None, None, None) == -1
+    assert "negative" in _err()
+    assert lib.t2t_token_inputs(P, P, 4, None, None, 0, None, 1, 64, 9, P, P, P, None) == -2
+    assert "words" in _err()
+    assert lib.t2t_token_inputs(P, P, 4, None, None, 0, None, 1, 64, 0, None, None, None,
+                                None) == -1
+    assert "doc" in _err()
+    # grants without their count, and grant words without words
+    assert lib.t2t_token_inputs(P, P, 4, P, None, 8, None, 1, 64, 1, P, P, P, None) == -1
+    assert "both" in _err()
+    assert lib.t2t_token_inputs(P, P, 4, P, P, 8, None, 1, 64, 0, P, None, None, None) == -1
+    assert "words > 0" in _err()
+    assert lib.t2t_token_inputs(P, P, 4, None, None, 0, None, 1, 64, 2, P, None, P, None) == -1
+    assert "q_bits" in _err()

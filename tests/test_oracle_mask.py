@@ -162,22 +162,36 @@ class _NoDetector:
         return span.raw_identifier
 
 
+def _paint(seq_len, ranges, words):
+    """Grant ranges -> uint64 [words, T] words (bit k of word k // 64)."""
+    qb = np.zeros((words, seq_len), dtype=np.uint64)
+    kb = np.zeros((words, seq_len), dtype=np.uint64)
+    for bit, qs, qe, ks, ke in ranges:
+        m = np.uint64(1) << np.uint64(bit % 64)
+        qb[bit // 64, max(0, qs):min(seq_len, qe)] |= m
+        kb[bit // 64, max(0, ks):min(seq_len, ke)] |= m
+    return qb, kb
+
+
 @pytest.mark.parametrize("seed", range(20))
-def test_host_grant_builder_matches_oracle(seed):
+def test_host_grant_ranges_match_oracle(seed):
     seq_len, spans, l2t = _random_scenario(random.Random(100 + seed))
     creator = CrossDocLinkMaskCreator(_NoDetector(), max_grants=128)
-    qb, kb, n = creator._build_grant_bitmasks(seq_len, spans, l2t)
+    ranges = creator._grant_ranges(seq_len, spans, l2t)
+    assert [r[0] for r in ranges] == list(range(len(ranges)))  # consecutive grant indices
+    qb, kb = _paint(seq_len, ranges, 2)
     oq, ok, on = mo.build_grant_bitmasks(seq_len, spans, l2t, 2, 128)
-    assert n == on and np.array_equal(qb, oq) and np.array_equal(kb, ok)
+    assert len(ranges) == on and np.array_equal(qb, oq) and np.array_equal(kb, ok)
 
 
 @pytest.mark.parametrize("n_grants,max_grants", [(65, 64), (257, 256), (129, 256)])
-def test_host_grant_builder_truncates_like_oracle(n_grants, max_grants):
+def test_host_grant_ranges_truncate_like_oracle(n_grants, max_grants):
     seq_len, spans, l2t = _n_grant_scenario(n_grants)
     creator = CrossDocLinkMaskCreator(_NoDetector(), max_grants=max_grants)
-    qb, kb, n = creator._build_grant_bitmasks(seq_len, spans, l2t)
+    ranges = creator._grant_ranges(seq_len, spans, l2t)
+    qb, kb = _paint(seq_len, ranges, creator._n_chunks)
     oq, ok, on = mo.build_grant_bitmasks(seq_len, spans, l2t, creator._n_chunks, max_grants)
-    assert n == on == min(n_grants, max_grants)
+    assert len(ranges) == on == min(n_grants, max_grants)
     assert np.array_equal(qb, oq) and np.array_equal(kb, ok)
 
 
