@@ -6,9 +6,12 @@ Seams replaced (reference file:line):
     the module-global symbol the reference's attention module calls
     (model/modules/layer.py:16-21,33; monkey-patched at generate.py:167-178),
     i.e. torch/nn/attention/flex_attention.py:1396-1676.
-  * ``T2TFlexAttentionFn`` -- in place of FlexAttentionAutogradOp
-    (torch/_higher_order_ops/flex_attention.py:628-767): saves q, k, v, out and
-    the log2-domain LSE; backward runs the atomic-free dK/dV + dQ kernels.
+  * ``torch.ops.t2t.masked_attention`` -- in place of FlexAttentionAutogradOp
+    (torch/_higher_order_ops/flex_attention.py:628-767): a ``torch.library``
+    custom op (fake implementation + registered autograd, so compiled models
+    trace it) that saves q, k, v, out and the log2-domain LSE; its backward is
+    the custom op ``t2t::masked_attention_backward`` (atomic-free dK/dV + dQ
+    kernels).  ``T2TFlexAttentionFn`` is the same as a plain autograd.Function.
   * ``FlexSelfAttention(dim, num_heads, max_seq_len, fp8_out_proj)`` with
     ``forward(x, block_mask)`` -- the constructor / call signature the
     reference's Layer uses (model/modules/layer.py:16-21,33).
@@ -25,7 +28,9 @@ import torch
 import torch.nn as nn
 
 from . import _lib
-from .block_mask import T2TBlockMask
+from typing import List, Tuple
+
+from .block_mask import T2TBlockMask, tables_c_struct
 
 LN2 = math.log(2.0)
 _DTYPE_CODES = {torch.bfloat16: _lib.T2T_DTYPE_BF16}
@@ -84,8 +89,16 @@ def _validate(q, k, v, block_mask, enable_gqa):
     return B, Hq, Hkv, T, D
 
 
-def attn_fwd(q, k, v, block_mask: T2TBlockMask, scale: float):
-    """Kernel call: returns (out [B,Hq,T,D] in q.dtype, lse2 float32 [B,Hq,T])."""
+def _mask_struct(block_mask):
+    """struct t2t_block_mask of a T2TBlockMask or of its list of tables."""
+    if isinstance(block_mask, T2TBlockMask):
+        return block_mask.c_struct()
+    return tables_c_struct(block_mask)
+
+
+def attn_fwd(q, k, v, block_mask, scale: float):
+    """Kernel call: returns (out [B,Hq,T,D] in q.dtype, lse2 float32 [B,Hq,T]).
+    ``block_mask``: a T2TBlockMask or its ``tables()`` list."""
     B, Hq, Hkv, T, D = q.shape[0], q.shape[1], k.shape[1], q.shape[2], q.shape[3]
     out = torch.empty((B, Hq, T, D), dtype=q.dtype, device=q.device)
     lse2 = torch.empty((B, Hq, T), dtype=torch.float32, device=q.device)
@@ -94,13 +107,13 @@ def attn_fwd(q, k, v, block_mask: T2TBlockMask, scale: float):
         rc = _lib.lib().t2t_attn_fwd(ctypes.byref(qs), ctypes.byref(ks), ctypes.byref(vs),
                                      ctypes.byref(os_), lse2.data_ptr(), B, Hq, Hkv, T, D,
                                      _DTYPE_CODES[q.dtype], float(scale),
-                                     ctypes.byref(block_mask.c_struct()), _stream_ptr(q))
+                                     ctypes.byref(_mask_struct(block_mask)), _stream_ptr(q))
     _lib.check(rc, "t2t_attn_fwd")
     return out, lse2
 
 
-def attn_bwd(q, k, v, out, dout, lse2, block_mask: T2TBlockMask, scale: float):
-    """Kernel call: returns (dq, dk, dv)."""
+def attn_bwd(q, k, v, out, dout, lse2, block_mask, scale: float):
+    """Kernel call: returns (dq, dk, dv).  ``block_mask`` as in attn_fwd."""
     B, Hq, Hkv, T, D = q.shape[0], q.shape[1], k.shape[1], q.shape[2], q.shape[3]
     if dout.stride(3) != 1:
         dout = dout.contiguous()
@@ -114,7 +127,7 @@ def attn_bwd(q, k, v, out, dout, lse2, block_mask: T2TBlockMask, scale: float):
         rc = _lib.lib().t2t_attn_bwd(*[ctypes.byref(x) for x in views], lse2.data_ptr(),
                                      delta.data_ptr(), *[ctypes.byref(x) for x in gviews],
                                      B, Hq, Hkv, T, D, _DTYPE_CODES[q.dtype], float(scale),
-                                     ctypes.byref(block_mask.c_struct()), _stream_ptr(q))
+                                     ctypes.byref(_mask_struct(block_mask)), _stream_ptr(q))
     _lib.check(rc, "t2t_attn_bwd")
     return dq, dk, dv
 
@@ -186,6 +199,52 @@ class T2TFlexAttentionFn(torch.autograd.Function):
         return dq, dk, dv, None, None
 
 
+@torch.library.custom_op("t2t::masked_attention", mutates_args=())
+def masked_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                     tables: List[torch.Tensor], scale: float) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Masked attention forward on the gfx950 kernels: (out, lse2).  ``tables``
+    = T2TBlockMask.tables() (the mask as tensors, so the op has a schema)."""
+    return attn_fwd(q, k, v, tables, scale)
+
+
+@masked_attention.register_fake
+def _masked_attention_fake(q, k, v, tables, scale):
+    B, Hq, T, D = q.shape
+    return (q.new_empty((B, Hq, T, D)), q.new_empty((B, Hq, T), dtype=torch.float32))
+
+
+@torch.library.custom_op("t2t::masked_attention_backward", mutates_args=())
+def masked_attention_backward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                              out: torch.Tensor, dout: torch.Tensor, lse2: torch.Tensor,
+                              tables: List[torch.Tensor],
+                              scale: float) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """(dq, dk, dv) on the gfx950 kernels (Delta, dK/dV, dQ launches)."""
+    return attn_bwd(q, k, v, out, dout, lse2, tables, scale)
+
+
+@masked_attention_backward.register_fake
+def _masked_attention_backward_fake(q, k, v, out, dout, lse2, tables, scale):
+    return (torch.empty_like(q, memory_format=torch.contiguous_format),
+            torch.empty_like(k, memory_format=torch.contiguous_format),
+            torch.empty_like(v, memory_format=torch.contiguous_format))
+
+
+def _masked_attention_setup(ctx, inputs, output):
+    q, k, v, tables, scale = inputs
+    out, lse2 = output
+    ctx.save_for_backward(q, k, v, out, lse2, *tables)
+    ctx.scale = scale
+
+
+def _masked_attention_bwd(ctx, dout, _dlse2):
+    q, k, v, out, lse2, *tables = ctx.saved_tensors
+    dq, dk, dv = masked_attention_backward(q, k, v, out, dout.contiguous(), lse2, tables, ctx.scale)
+    return dq, dk, dv, [None] * len(tables), None
+
+
+masked_attention.register_autograd(_masked_attention_bwd, setup_context=_masked_attention_setup)
+
+
 def flex_attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
                    score_mod=None, block_mask: Optional[T2TBlockMask] = None,
                    scale: Optional[float] = None, enable_gqa: bool = False,
@@ -203,7 +262,7 @@ def flex_attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
     _, _, _, _, D = _validate(query, key, value, block_mask, enable_gqa)
     if scale is None:
         scale = 1.0 / math.sqrt(D)  # torch/nn/attention/flex_attention.py:1544
-    out, lse2 = T2TFlexAttentionFn.apply(query, key, value, block_mask, float(scale))
+    out, lse2 = masked_attention(query, key, value, block_mask.tables(), float(scale))
     if return_lse:
         return out, lse2 * LN2
     return out

@@ -72,13 +72,16 @@ class T2TBlockMask:
     def seq_lengths(self):
         return (self.seq_len, self.seq_len)
 
+    def tables(self):
+        """The 13 device tables the kernels read, in t2t_block_mask order."""
+        return [self.kv_num_blocks, self.kv_indices, self.full_kv_num_blocks,
+                self.full_kv_indices, self.q_num_blocks, self.q_indices, self.full_q_num_blocks,
+                self.full_q_indices, self.row_order, self.col_order, self.kv_bits_off,
+                self.q_bits_slot, self.tile_bits]
+
     def c_struct(self) -> _lib.T2TBlockMaskC:
         if self._c is None:
-            self._c = _c_struct(self.mask_batch, self.num_tiles, self.kv_num_blocks,
-                                self.kv_indices, self.full_kv_num_blocks, self.full_kv_indices,
-                                self.q_num_blocks, self.q_indices, self.full_q_num_blocks,
-                                self.full_q_indices, self.row_order, self.col_order,
-                                self.kv_bits_off, self.q_bits_slot, self.tile_bits)
+            self._c = tables_c_struct(self.tables())
         return self._c
 
     def mask_mod(self):
@@ -110,10 +113,11 @@ class T2TBlockMask:
         return 100.0 * float((tc == 0).sum().item()) / max(1, tc.numel())
 
 
-def _c_struct(Bm, nt, *tensors) -> _lib.T2TBlockMaskC:
-    ptrs = [t.data_ptr() for t in tensors]
-    tile_bits = tensors[-1]
-    return _lib.T2TBlockMaskC(Bm, nt, *ptrs, tile_bits.shape[0])
+def tables_c_struct(tables) -> _lib.T2TBlockMaskC:
+    """struct t2t_block_mask over the 13 tables of T2TBlockMask.tables()."""
+    kv_num = tables[0]
+    Bm, nt = int(kv_num.shape[0]), int(kv_num.shape[-1])
+    return _lib.T2TBlockMaskC(Bm, nt, *[t.data_ptr() for t in tables], tables[-1].shape[0])
 
 
 def _as_words(bits: Optional[torch.Tensor], Bm: int, T: int, device) -> torch.Tensor:
@@ -166,7 +170,7 @@ def build_block_mask(doc_ids: torch.Tensor, q_bits: Optional[torch.Tensor] = Non
     tabs = (t["kv_num"], t["kv_idx"], t["full_kv_num"], t["full_kv_idx"], t["q_num"], t["q_idx"],
             t["full_q_num"], t["full_q_idx"], row_order, col_order, kv_bits_off, q_bits_slot,
             tile_bits)
-    cs = _c_struct(Bm, nt, *tabs)
+    cs = tables_c_struct(tabs)
     s = stream if stream is not None else torch.cuda.current_stream(device)
     with torch.cuda.device(device):
         rc = _lib.lib().t2t_mask_meta(
