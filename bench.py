@@ -144,12 +144,69 @@ def cpu_baseline(rows_np, c, seed, threads):
     return t_step, t_mask, t_head
 
 
+def backbone_step(args, dev):
+    """one training step (mask creation from the device-resident
+    span / link lists, embedding, 12 layers, RMSNorm, tied linear + CE loss,
+    backward, AdamW) of the 12-layer d768 H12 (D 64) backbone on a packed
+    T = 16384 row of random token ids with the configs[2] cross_doc_link
+    generator; random-init weights.  Prints one JSON line (tokens/s)."""
+    from tagseq2tagseq_amd.modules import TS2TSTrainingModule
+    T, V = 16384, 50257
+    row = synth.config_rows(3, seed=args.seed)[0]
+    lists = TokenLists(T, [row.spans], dev, words=row.words, link_rows=[row.link_rows])
+
+    def creator(tokens, **kw):
+        return build_block_mask(*lists.build())
+
+    torch.manual_seed(args.seed)
+    model = TS2TSTrainingModule.from_config(
+        vocab_size=V, num_layers=12, model_dim=768, num_heads=12, max_seq_len=T, dropout=0.0,
+        drop_path_rate=0.0, block_mask_creator=creator).to(dev, torch.bfloat16)
+    opt = torch.optim.AdamW(model.parameters(), lr=1e-4, foreach=True)
+    g = torch.Generator().manual_seed(args.seed)
+    tokens = torch.randint(0, V, (1, T + 1), generator=g).to(dev)
+    batch = {"tokens": tokens}
+
+    def step():
+        loss = model(batch)
+        loss.backward()
+        opt.step()
+        opt.zero_grad(set_to_none=True)
+        return loss
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    ev0.record()
+    for _ in range(args.steps):
+        loss = step()
+    ev1.record()
+    torch.cuda.synchronize()
+    ms = ev0.elapsed_time(ev1) / args.steps
+    n_params = sum(p.numel() for p in model.parameters())
+    print(json.dumps({
+        "metric": "backbone training tokens/s (12L d768 H12 D64, cross_doc_link T=16k)",
+        "value": round(T / (ms * 1e-3), 1), "unit": "tokens/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 3),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (random token ids, seeded packed documents)",
+        "config": {"workload": "12-layer backbone training step (configs[4])", "T": T,
+                   "vocab": V, "params": n_params, "n_docs": row.n_docs,
+                   "optimizer": "AdamW (foreach)"},
+        "final_loss": round(float(loss.item()), 4),
+    }))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", type=int, default=3, choices=[2, 3, 4])
+    ap.add_argument("--config", type=int, default=3, choices=[2, 3, 4, 5],
+                    help="3 (default): the metric's workload; 2, 4: other attention "
+                         "workloads; 5: 12-layer backbone training step (tokens/s)")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--reps", type=int, default=20, help="launches per per-kernel timing")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -166,6 +223,10 @@ def main():
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         sys.exit(2)
     dev = torch.device("cuda:0")
+
+    if args.config == 5:
+        backbone_step(args, dev)
+        return
 
     if args.copy_calibration:
         x = torch.empty(1 << 30, dtype=torch.uint8, device=dev).fill_(1)
