@@ -144,6 +144,50 @@ def cpu_baseline(rows_np, c, seed, threads):
     return t_step, t_mask, t_head
 
 
+def prologue_stats(dev, T: int, C: int, H: int, reps: int):
+    """HIP-event timing of the attention-module prologue (t2t_qkv_rope and its
+    gradient pass) at one layer's shape.  Algorithmic bytes per launch: the
+    bf16 qkv rows read once and the q, k, v rows written once (2 x 3 C T x 2 B),
+    plus the float32 cos / sin rows of the T positions (2 x T x D/2 x 4 B)."""
+    import ctypes
+    from tagseq2tagseq_amd import _lib
+    from tagseq2tagseq_amd.rope import rope_tables
+    D = C // H
+    g = torch.Generator().manual_seed(0)
+    qkv = torch.randn(1, T, 3 * C, generator=g).to(torch.bfloat16).to(dev)
+    dqkv = torch.empty_like(qkv)
+    cos, sin = rope_tables(D, T, dev)
+    ops = [torch.empty(1, H, T, D, dtype=torch.bfloat16, device=dev) for _ in range(3)]
+    views = [ctypes.byref(_lib.tensor_struct(t)) for t in ops]
+    stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+    L = _lib.lib()
+    # Launch through the C ABI with preallocated buffers, so the loop times the
+    # kernels rather than the Python dispatch around them.
+    calls = {
+        "fwd": lambda: L.t2t_qkv_rope(qkv.data_ptr(), qkv.stride(0), qkv.stride(1), 1, T, H, D,
+                                      cos.data_ptr(), sin.data_ptr(), T, 0, *views, stream),
+        "bwd": lambda: L.t2t_qkv_rope_backward(*views, cos.data_ptr(), sin.data_ptr(), T, 0, 1,
+                                               T, H, D, dqkv.data_ptr(), dqkv.stride(0),
+                                               dqkv.stride(1), stream),
+    }
+    nbytes = 2 * 3 * C * T * 2 + 2 * T * (D // 2) * 4
+    out = {"shape": {"T": T, "C": C, "H": H, "D": D}, "bytes_per_launch": nbytes}
+    for name, fn in calls.items():
+        _lib.check(fn(), "t2t_qkv_rope " + name)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        us = 1e3 * e0.elapsed_time(e1) / reps
+        gbps = nbytes / (us * 1e-6) / 1e9
+        out[name] = {"us": round(us, 2), "GBps": round(gbps, 1),
+                     "frac_of_hbm_peak": round(gbps / PEAK_HBM_GBS, 3)}
+    return out
+
+
 def backbone_step(args, dev):
     """one training step (mask creation from the device-resident
     span / link lists, embedding, 12 layers, RMSNorm, tied linear + CE loss,
@@ -186,6 +230,7 @@ def backbone_step(args, dev):
     torch.cuda.synchronize()
     ms = ev0.elapsed_time(ev1) / args.steps
     n_params = sum(p.numel() for p in model.parameters())
+    prologue = prologue_stats(dev, T, 768, 12, args.reps)
     print(json.dumps({
         "metric": "backbone training tokens/s (12L d768 H12 D64, cross_doc_link T=16k)",
         "value": round(T / (ms * 1e-3), 1), "unit": "tokens/s", "n_gpus": 1,
@@ -196,6 +241,7 @@ def backbone_step(args, dev):
                    "vocab": V, "params": n_params, "n_docs": row.n_docs,
                    "optimizer": "AdamW (foreach)"},
         "final_loss": round(float(loss.item()), 4),
+        "prologue": prologue,
     }))
 
 

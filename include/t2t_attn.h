@@ -190,6 +190,38 @@ int t2t_attn_bwd_dq(const t2t_tensor *q, const t2t_tensor *k, const t2t_tensor *
                     int32_t D, int32_t dtype, float scale, const t2t_block_mask *mask,
                     void *stream);
 
+/*
+ * Attention-module prologue: QKV split + rotary embedding.  Replaces the
+ * head split and rotary embedding inside the reference's attention module
+ * (tunalab FlexSelfAttention as constructed and called at
+ * model/modules/layer.py:16-21,33; that package's source is not in the
+ * reference, so the rotary variant is the half-split form below).
+ *   qkv   bf16 [B][T][3][H][D]: token rows of 3*H*D elements with element
+ *         strides qkv_sb (batch) and qkv_st (token); within a row q, k, v
+ *         head blocks are contiguous (the nn.Linear(C, 3C) output viewed as
+ *         [B, T, 3, H, D]).
+ *   cos, sin  float [table_rows][D/2] (contiguous); token t uses row pos0 + t.
+ *   q, k, v   [B, H, T, D] outputs: for i < D/2, with c, s = cos, sin[pos0 + t][i],
+ *             y[i] = x[i] c + x[i + D/2] s,  y[i + D/2] = x[i + D/2] c - x[i] s
+ *             on q and k (fp32 arithmetic, one bf16 rounding); v is copied.
+ * Supported: bf16, D % 16 == 0 and D <= 256; rows and views 16-byte aligned.
+ */
+int t2t_qkv_rope(const void *qkv, int64_t qkv_sb, int64_t qkv_st, int32_t B, int32_t T,
+                 int32_t H, int32_t D, const float *cos, const float *sin, int32_t table_rows,
+                 int32_t pos0, const t2t_tensor *q, const t2t_tensor *k, const t2t_tensor *v,
+                 void *stream);
+
+/*
+ * Gradient of t2t_qkv_rope: dqkv (layout of qkv) from dq, dk, dv, applying the
+ * transposed rotation dx[i] = dy[i] c - dy[i + D/2] s,
+ * dx[i + D/2] = dy[i] s + dy[i + D/2] c to dq and dk and copying dv.  Every
+ * element of dqkv is written (not accumulated).
+ */
+int t2t_qkv_rope_backward(const t2t_tensor *dq, const t2t_tensor *dk, const t2t_tensor *dv,
+                          const float *cos, const float *sin, int32_t table_rows, int32_t pos0,
+                          int32_t B, int32_t T, int32_t H, int32_t D, void *dqkv,
+                          int64_t dqkv_sb, int64_t dqkv_st, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

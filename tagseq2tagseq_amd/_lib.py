@@ -39,6 +39,7 @@ _lib = None
 
 _P = ctypes.c_void_p
 _I32 = ctypes.c_int32
+_I64 = ctypes.c_int64
 _SIGS = {
     "t2t_version": ([], ctypes.c_char_p),
     "t2t_last_error": ([], ctypes.c_char_p),
@@ -50,6 +51,9 @@ _SIGS = {
     "t2t_attn_bwd_preprocess": ([_P] * 3 + [_I32] * 5 + [_P], ctypes.c_int),
     "t2t_attn_bwd_dkdv": ([_P] * 8 + [_I32] * 6 + [ctypes.c_float, _P, _P], ctypes.c_int),
     "t2t_attn_bwd_dq": ([_P] * 7 + [_I32] * 6 + [ctypes.c_float, _P, _P], ctypes.c_int),
+    "t2t_qkv_rope": ([_P, _I64, _I64] + [_I32] * 4 + [_P, _P, _I32, _I32] + [_P] * 4,
+                     ctypes.c_int),
+    "t2t_qkv_rope_backward": ([_P] * 5 + [_I32] * 6 + [_P, _I64, _I64, _P], ctypes.c_int),
 }
 
 

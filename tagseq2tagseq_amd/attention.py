@@ -100,7 +100,9 @@ def attn_fwd(q, k, v, block_mask, scale: float):
     """Kernel call: returns (out [B,Hq,T,D] in q.dtype, lse2 float32 [B,Hq,T]).
     ``block_mask``: a T2TBlockMask or its ``tables()`` list."""
     B, Hq, Hkv, T, D = q.shape[0], q.shape[1], k.shape[1], q.shape[2], q.shape[3]
-    out = torch.empty((B, Hq, T, D), dtype=q.dtype, device=q.device)
+    # [B, T, Hq, D] storage seen as [B, Hq, T, D]: the module's output
+    # projection then reads token rows without a transpose copy.
+    out = torch.empty((B, T, Hq, D), dtype=q.dtype, device=q.device).transpose(1, 2)
     lse2 = torch.empty((B, Hq, T), dtype=torch.float32, device=q.device)
     qs, ks, vs, os_ = _view(q), _view(k), _view(v), _view(out)
     with torch.cuda.device(q.device):
@@ -210,7 +212,8 @@ def masked_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
 @masked_attention.register_fake
 def _masked_attention_fake(q, k, v, tables, scale):
     B, Hq, T, D = q.shape
-    return (q.new_empty((B, Hq, T, D)), q.new_empty((B, Hq, T), dtype=torch.float32))
+    return (q.new_empty((B, T, Hq, D)).transpose(1, 2),
+            q.new_empty((B, Hq, T), dtype=torch.float32))
 
 
 @torch.library.custom_op("t2t::masked_attention_backward", mutates_args=())
@@ -269,22 +272,19 @@ def flex_attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
 
 
 class Rotary(nn.Module):
-    """Rotary position embedding on [B, H, T, D] (half-split pairs, base 10000)."""
+    """Rotary-embedding tables for [B, H, T, D] heads: half-split pairs, base
+    10000, position = token index (float32 [max_seq_len, D/2] cos / sin, kept
+    in float32 whatever dtype the module is cast to)."""
 
     def __init__(self, head_dim: int, max_seq_len: int, base: float = 10000.0):
         super().__init__()
-        inv = base ** (-torch.arange(0, head_dim // 2, dtype=torch.float32) / (head_dim // 2))
-        t = torch.arange(max_seq_len, dtype=torch.float32)
-        freqs = torch.outer(t, inv)
-        self.register_buffer("cos", freqs.cos(), persistent=False)
-        self.register_buffer("sin", freqs.sin(), persistent=False)
+        self.head_dim = head_dim
+        self.max_seq_len = max_seq_len
+        self.base = base
 
-    def forward(self, x: torch.Tensor) -> torch.Tensor:
-        T = x.shape[-2]
-        cos = self.cos[:T].to(x.dtype)
-        sin = self.sin[:T].to(x.dtype)
-        x1, x2 = x.chunk(2, dim=-1)
-        return torch.cat((x1 * cos + x2 * sin, x2 * cos - x1 * sin), dim=-1)
+    def tables(self, device):
+        from .rope import rope_tables
+        return rope_tables(self.head_dim, self.max_seq_len, device, self.base)
 
 
 class FlexSelfAttention(nn.Module):
@@ -292,9 +292,12 @@ class FlexSelfAttention(nn.Module):
     Layer uses (model/modules/layer.py:16-21, 33): QKV projection, rotary
     embedding, masked attention on the gfx950 kernels, output projection.
 
-    The reference's module comes from the absent ``tunalab`` package; its
-    internal details (RoPE variant, QK-norm, fp8 out-projection) are not
-    available here, so ``fp8_out_proj`` is accepted and ignored.
+    The head split and rotation run as one prologue kernel (t2t::qkv_rope);
+    the attention output is produced in [B, T, H, D] order, so the output
+    projection reads it without a transpose copy.  The reference's module
+    comes from the absent ``tunalab`` package; its internal details (RoPE
+    variant, QK-norm, fp8 out-projection) are not available here, so
+    ``fp8_out_proj`` is accepted and ignored.
     """
 
     def __init__(self, dim: int, num_heads: int, max_seq_len: int, fp8_out_proj: bool = False):
@@ -310,11 +313,9 @@ class FlexSelfAttention(nn.Module):
         self.fp8_out_proj = fp8_out_proj
 
     def forward(self, x: torch.Tensor, block_mask: T2TBlockMask) -> torch.Tensor:
+        from .rope import qkv_rope
         B, T, C = x.shape
-        qkv = self.qkv(x).view(B, T, 3, self.num_heads, self.head_dim)
-        q, k, v = qkv.unbind(dim=2)
-        q = self.rotary(q.transpose(1, 2))
-        k = self.rotary(k.transpose(1, 2))
-        v = v.transpose(1, 2)
+        cos, sin = self.rotary.tables(x.device)
+        q, k, v = qkv_rope(self.qkv(x), cos, sin, self.num_heads)
         y = flex_attention(q, k, v, block_mask=block_mask)
         return self.proj(y.transpose(1, 2).reshape(B, T, C))

@@ -81,4 +81,15 @@ hipError_t launch_attn_bwd_phase(int phase, const TensorView& q, const TensorVie
                                  const AttnDims& dims, const MaskTables& mask,
                                  hipStream_t stream);
 
+// Attention-module prologue: qkv [B][T][3][H][D] rows (strides sb, st) to
+// rotated q, k and plain v views, and the transposed map for the gradients.
+hipError_t launch_qkv_rope(const __bf16* qkv, int64_t sb, int64_t st, const TensorView& q,
+                           const TensorView& k, const TensorView& v, const float* cos,
+                           const float* sin, int B, int T, int H, int D, int pos0,
+                           hipStream_t stream);
+hipError_t launch_qkv_rope_bwd(const TensorView& dq, const TensorView& dk, const TensorView& dv,
+                               const float* cos, const float* sin, int B, int T, int H, int D,
+                               int pos0, __bf16* dqkv, int64_t sb, int64_t st,
+                               hipStream_t stream);
+
 }  // namespace t2t

@@ -253,4 +253,66 @@ int t2t_attn_bwd(const t2t_tensor* q, const t2t_tensor* k, const t2t_tensor* v,
                          stream);
 }
 
+namespace {
+
+// A [B, H, T, D] view the prologue kernels address with 16-byte vector
+// accesses (plain global pointers, so no 2 GiB slice limit).
+bool rope_view_ok(const t2t_tensor* t) {
+  return t && t->data && (reinterpret_cast<uintptr_t>(t->data) % 16) == 0 && t->stride_b >= 0 &&
+         t->stride_h >= 0 && t->stride_t > 0 && (t->stride_b % 8) == 0 &&
+         (t->stride_h % 8) == 0 && (t->stride_t % 8) == 0;
+}
+
+int check_rope(int B, int T, int H, int D, const float* cos, const float* sin, int table_rows,
+               int pos0, const void* packed, int64_t sb, int64_t st) {
+  if (B < 0 || T < 0 || H < 0 || table_rows < 0 || pos0 < 0)
+    return fail(T2T_EINVAL, "negative B, T, H, table_rows or pos0");
+  if (D < 16 || D > 256 || D % 16 != 0)
+    return fail(T2T_EUNSUPPORTED, "head dim %d is not a multiple of 16 in [16, 256]", D);
+  if (B == 0 || T == 0 || H == 0) return T2T_OK;
+  if ((int64_t)pos0 + T > table_rows)
+    return fail(T2T_EINVAL, "positions %d..%d exceed the %d table rows", pos0, pos0 + T - 1,
+                table_rows);
+  if (!cos || !sin || !packed) return fail(T2T_EINVAL, "cos, sin or the packed qkv is NULL");
+  if ((reinterpret_cast<uintptr_t>(cos) | reinterpret_cast<uintptr_t>(sin) |
+       reinterpret_cast<uintptr_t>(packed)) % 16)
+    return fail(T2T_EINVAL, "cos, sin and the packed qkv must be 16-byte aligned");
+  if (sb < 0 || st < 0 || sb % 8 || st % 8)
+    return fail(T2T_EINVAL, "packed strides must be non-negative multiples of 8 elements");
+  if (T > 1 && st < 3LL * H * D)
+    return fail(T2T_EINVAL, "packed token stride %lld is below 3*H*D = %lld", (long long)st,
+                3LL * H * D);
+  return T2T_OK;
+}
+
+}  // namespace
+
+int t2t_qkv_rope(const void* qkv, int64_t qkv_sb, int64_t qkv_st, int32_t B, int32_t T,
+                 int32_t H, int32_t D, const float* cos, const float* sin, int32_t table_rows,
+                 int32_t pos0, const t2t_tensor* q, const t2t_tensor* k, const t2t_tensor* v,
+                 void* stream) {
+  int rc = check_rope(B, T, H, D, cos, sin, table_rows, pos0, qkv, qkv_sb, qkv_st);
+  if (rc || B == 0 || T == 0 || H == 0) return rc;
+  if (!rope_view_ok(q) || !rope_view_ok(k) || !rope_view_ok(v))
+    return fail(T2T_EINVAL, "q/k/v view invalid (NULL, misaligned or bad stride)");
+  return hip_status(t2t::launch_qkv_rope(static_cast<const __bf16*>(qkv), qkv_sb, qkv_st,
+                                         as_view(q), as_view(k), as_view(v), cos, sin, B, T, H,
+                                         D, pos0, static_cast<hipStream_t>(stream)),
+                    "t2t_qkv_rope launch");
+}
+
+int t2t_qkv_rope_backward(const t2t_tensor* dq, const t2t_tensor* dk, const t2t_tensor* dv,
+                          const float* cos, const float* sin, int32_t table_rows, int32_t pos0,
+                          int32_t B, int32_t T, int32_t H, int32_t D, void* dqkv,
+                          int64_t dqkv_sb, int64_t dqkv_st, void* stream) {
+  int rc = check_rope(B, T, H, D, cos, sin, table_rows, pos0, dqkv, dqkv_sb, dqkv_st);
+  if (rc || B == 0 || T == 0 || H == 0) return rc;
+  if (!rope_view_ok(dq) || !rope_view_ok(dk) || !rope_view_ok(dv))
+    return fail(T2T_EINVAL, "dq/dk/dv view invalid (NULL, misaligned or bad stride)");
+  return hip_status(t2t::launch_qkv_rope_bwd(as_view(dq), as_view(dk), as_view(dv), cos, sin, B,
+                                             T, H, D, pos0, static_cast<__bf16*>(dqkv), dqkv_sb,
+                                             dqkv_st, static_cast<hipStream_t>(stream)),
+                    "t2t_qkv_rope_backward launch");
+}
+
 }  // extern "C"

@@ -31,8 +31,8 @@ WORKLOADS = {
 
 
 def _short(name: str) -> str:
-    """Kernel name without the template / argument decoration."""
-    base = name.split("(")[0]
+    """Kernel name without the namespace / template / argument decoration."""
+    base = name.replace("(anonymous namespace)", "").split("(")[0]
     if "<" in base:
         base = base.split("<")[0]
     return base.split("::")[-1].replace("void ", "").strip()
@@ -88,8 +88,9 @@ def trace(kt_dir: str, bench_json: str, cfg: int) -> str:
         f"#   rocprofv3 --kernel-trace --stats -d {kt_dir} -o kt -- \\",
         f"#       python -u bench.py --config {cfg} --no-cpu-baseline --steps 10 --warmup 3",
         "# durations in microseconds over every dispatch of the run (warm-up, timed steps and",
-        "# bench.py's per-kernel timing loops); bench.py's own HIP-event means for the same",
-        "# build (separate run, no profiler) are listed for comparison.",
+        "# bench.py's per-kernel timing loops); the last column is bench.py's own HIP-event",
+        "# mean per call from the JSON line of the same profiled run (token_inputs: the whole",
+        "# TokenLists.build() call, host side included).",
         "",
         f"{'kernel':28s} {'calls':>6s} {'mean':>8s} {'median':>8s} {'min':>8s} {'max':>8s}   bench.py HIP events",
     ]

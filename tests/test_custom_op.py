@@ -24,3 +24,28 @@ def test_schemas():
     assert "Tensor[] tables" in s and "float scale" in s
     s = str(torch.ops.t2t.masked_attention_backward.default._schema)
     assert s.count("Tensor") >= 7
+
+
+def test_qkv_rope_fake_shapes_and_schema():
+    import tagseq2tagseq_amd.rope  # noqa: F401  (registers torch.ops.t2t.qkv_rope*)
+    with FakeTensorMode():
+        qkv = torch.empty(2, 96, 3 * 12 * 64, dtype=torch.bfloat16)
+        cos = torch.empty(128, 32)
+        q, k, v = torch.ops.t2t.qkv_rope(qkv, cos, cos, 12, 0)
+        assert q.shape == k.shape == v.shape == (2, 12, 96, 64)
+        dqkv = torch.ops.t2t.qkv_rope_backward(q, k, v, cos, cos, 0)
+        assert dqkv.shape == qkv.shape and dqkv.dtype == torch.bfloat16
+    s = str(torch.ops.t2t.qkv_rope.default._schema)
+    assert "num_heads" in s and "pos0" in s
+
+
+def test_attention_output_is_token_major():
+    """The forward's output is [B, T, H, D] storage seen as [B, H, T, D], so the
+    module's transpose + reshape to [B, T, C] is a view."""
+    with FakeTensorMode():
+        q = torch.empty(1, 4, 256, 64, dtype=torch.bfloat16)
+        tables = [torch.empty(1, 1, 2, dtype=torch.int32) for _ in range(13)]
+        out, _ = torch.ops.t2t.masked_attention(q, q, q, tables, 0.125)
+        y = out.transpose(1, 2)
+        assert y.is_contiguous()
+        assert y.reshape(1, 256, 256).data_ptr() == out.data_ptr()

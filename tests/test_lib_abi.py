@@ -127,3 +127,34 @@ def test_token_inputs_argument_checks():
     assert "words > 0" in _err()
     assert lib.t2t_token_inputs(P, P, 4, None, None, 0, None, 1, 64, 2, P, None, P, None) == -1
     assert "q_bits" in _err()
+
+
+def test_qkv_rope_argument_checks():
+    lib = _lib.lib()
+    P = ctypes.c_void_p(0x1000)
+    view = _lib.T2TTensor(0x1000, 0, 64 * 32, 64)
+    bad = _lib.T2TTensor(0x1008, 0, 64 * 32, 64)  # misaligned
+    v = ctypes.byref(view)
+    # empty work is a no-op
+    assert lib.t2t_qkv_rope(None, 0, 0, 0, 32, 4, 64, None, None, 0, 0, None, None, None, None) == 0
+    assert lib.t2t_qkv_rope(P, 0, 768, 1, -1, 4, 64, P, P, 32, 0, v, v, v, None) == -1
+    assert "negative" in _err()
+    assert lib.t2t_qkv_rope(P, 0, 768, 1, 32, 4, 40, P, P, 32, 0, v, v, v, None) == -2
+    assert "multiple of 16" in _err()
+    # positions past the table
+    assert lib.t2t_qkv_rope(P, 0, 768, 1, 32, 4, 64, P, P, 40, 9, v, v, v, None) == -1
+    assert "table rows" in _err()
+    # token rows overlap (stride below 3 H D)
+    assert lib.t2t_qkv_rope(P, 0, 512, 1, 32, 4, 64, P, P, 32, 0, v, v, v, None) == -1
+    assert "3*H*D" in _err()
+    assert lib.t2t_qkv_rope(P, 0, 768, 1, 32, 4, 64, P, P, 32, 0, v, ctypes.byref(bad), v,
+                            None) == -1
+    assert "view" in _err()
+    assert lib.t2t_qkv_rope(P, 0, 768, 1, 32, 4, 64, None, P, 32, 0, v, v, v, None) == -1
+    assert "NULL" in _err()
+    assert lib.t2t_qkv_rope_backward(v, v, v, P, P, 32, 0, 1, 32, 4, 64, ctypes.c_void_p(0x1004),
+                                     0, 768, None) == -1
+    assert "aligned" in _err()
+    assert lib.t2t_qkv_rope_backward(v, v, None, P, P, 32, 0, 1, 32, 4, 64, P, 0, 768,
+                                     None) == -1
+    assert "view" in _err()
