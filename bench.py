@@ -188,6 +188,131 @@ def prologue_stats(dev, T: int, C: int, H: int, reps: int):
     return out
 
 
+def decode_bench(args, dev):
+    """Generation on the configs[4] model (12 layers, d768, H12, D64, vocab
+    50257, random init) over a T = 16384 - 64 token context packed with the
+    configs[2] cross_doc_link generator: after one prefill, each step appends a
+    token to the last document and asks for the last position's logits.
+      * cached: TS2TSModel.forward_inference_last (key/value cache, decode
+        kernel over the new row), `--steps` steps after `--warmup`;
+      * full recompute: TS2TSModel.forward_inference over the whole sequence,
+        the reference's per-token path (model/generation_loop.py:90-92), 3 steps;
+      * the decode attention kernel alone at one layer's shape (Tq 1, H 12,
+        D 64, all context keys): algorithmic bytes = allowed keys x H x 4 D
+        (K and V rows) + H x Tkv x (4 + 8 W) (mask inputs read per head)."""
+    import numpy as np
+    from tagseq2tagseq_amd.decode import attn_decode
+    from tagseq2tagseq_amd.mask_creators import create_doc_link_block_mask
+    from tagseq2tagseq_amd.model import TS2TSModel
+    T_max, V, H, D = 16384, 50257, 12, 64
+    row = synth.config_rows(3, seed=args.seed)[0]
+    T0 = T_max - 64
+    spans = [s for s in row.spans if s.start < T0]
+    last = spans[-1]
+    spans[-1] = synth.DocSpan(doc_id=last.doc_id, start=last.start, end=T0)
+    links = np.asarray(row.link_rows, dtype=np.uint64)[:len(spans)]
+    torch.manual_seed(args.seed)
+    model = TS2TSModel.from_config(vocab_size=V, num_layers=12, model_dim=768, num_heads=H,
+                                   max_seq_len=T_max, dropout=0.0, drop_path_rate=0.0,
+                                   block_mask_creator=create_doc_link_block_mask)
+    model = model.to(dev, torch.bfloat16).eval()
+    g = torch.Generator().manual_seed(args.seed)
+    stream = torch.randint(0, V, (1, T_max), generator=g).to(dev)
+
+    def grown(n):
+        sp = list(spans)
+        sp[-1] = synth.DocSpan(doc_id=last.doc_id, start=last.start, end=T0 + n)
+        return stream[:, :T0 + n], sp
+
+    tok, sp = grown(0)
+    model.forward_inference_last(tok, sp, doc_links=links)  # prefill
+    n_steps = min(args.steps, 60 - args.warmup)
+    for i in range(1, args.warmup + 1):
+        tok, sp = grown(i)
+        model.forward_inference_last(tok, sp, doc_links=links)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.warmup + 1, args.warmup + 1 + n_steps):
+        tok, sp = grown(i)
+        logits = model.forward_inference_last(tok, sp, doc_links=links)
+        logits.argmax().item()  # the sampler needs the row on the host
+    cached_ms = 1e3 * (time.perf_counter() - t0) / n_steps
+    # the same steps without the captured graph (eager launches)
+    model.use_graphs = False
+    t0 = time.perf_counter()
+    for i in range(args.warmup + 1, args.warmup + 1 + n_steps):
+        tok, sp = grown(i)
+        model.forward_inference_last(tok, sp, doc_links=links).argmax().item()
+    eager_ms = 1e3 * (time.perf_counter() - t0) / n_steps
+    model.use_graphs = True
+    tok, sp = grown(args.warmup + n_steps)
+    ref = model.forward_inference(tok, sp, doc_links=links)[:, -1:].float()
+    err = (logits.float() - ref).abs().max().item() / ref.abs().max().item()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(3):
+        model.forward_inference(tok, sp, doc_links=links)[0, -1].argmax().item()
+    full_ms = 1e3 * (time.perf_counter() - t0) / 3
+
+    # the decode kernel alone at one layer's shape
+    bm = create_doc_link_block_mask(tok, sp, doc_links=links)
+    T = tok.shape[1]
+    cache = model.kv_cache
+    q = torch.randn(1, H, 1, D, device=dev).to(torch.bfloat16)
+    pos = torch.tensor([[T - 1]], dtype=torch.int32, device=dev)
+    qd = bm.doc_ids[:, T - 1:T].contiguous()
+    qb = bm.q_bits[:, :, T - 1:T].contiguous()
+    kc, vc = cache.k[0], cache.v[0]
+    out = torch.empty(1, H, 1, D, dtype=torch.bfloat16, device=dev)
+    attn_decode(q, kc, vc, T, cache.doc, cache.kv_bits, pos, qd, qb, out=out)  # validates
+    # Launch through the C ABI with preallocated buffers so the loop times the
+    # kernels (partial + combine), not the Python wrapper.
+    import ctypes
+    from tagseq2tagseq_amd import _lib
+    L = _lib.lib()
+    lse2 = torch.empty(1, H, 1, dtype=torch.float32, device=dev)
+    wsb = L.t2t_attn_decode_workspace(1, H, 1, T, D)
+    ws = torch.empty(wsb // 4, dtype=torch.float32, device=dev)
+    views = [ctypes.byref(_lib.tensor_struct(t)) for t in (q, kc, vc, out)]
+    stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+    call_args = (*views, lse2.data_ptr(), cache.doc.data_ptr(), cache.kv_bits.data_ptr(),
+                 cache.doc.shape[1], pos.data_ptr(), qd.data_ptr(), qb.data_ptr(), 1, bm.words,
+                 1, H, H, 1, T, D, _lib.T2T_DTYPE_BF16, 1.0 / math.sqrt(D), ws.data_ptr(), wsb,
+                 stream)
+    _lib.check(L.t2t_attn_decode(*call_args), "t2t_attn_decode")
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(args.reps):
+        L.t2t_attn_decode(*call_args)
+    e1.record()
+    torch.cuda.synchronize()
+    k_us = 1e3 * e0.elapsed_time(e1) / args.reps
+    doc = bm.doc_ids[0]
+    allowed = (doc == doc[T - 1]) | ((bm.kv_bits[0] & bm.q_bits[0, :, T - 1:T]) != 0).any(0)
+    n_allowed = int(allowed.sum())
+    W = bm.words
+    k_bytes = n_allowed * H * 4 * D + H * T * (4 + 8 * W)
+    gbps = k_bytes / (k_us * 1e-6) / 1e9
+    print(json.dumps({
+        "metric": "generation tokens/s with the key/value cache (12L d768 H12 D64, "
+                  "cross_doc_link, T=16k context)",
+        "value": round(1e3 / cached_ms, 2), "unit": "tokens/s", "n_gpus": 1, "steps": n_steps,
+        "warmup": args.warmup, "ms_per_step": round(cached_ms, 3), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (random token ids, seeded packed documents, random-init weights)",
+        "config": {"workload": "decode steps on the configs[4] model", "context": T0,
+                   "vocab": V, "n_docs": len(spans), "grant_words": W},
+        "eager_cached_ms_per_token": round(eager_ms, 3),
+        "full_recompute_ms_per_token": round(full_ms, 2),
+        "speedup_vs_full_recompute": round(full_ms / cached_ms, 1),
+        "last_logits_rel_err_vs_full": round(err, 5),
+        "decode_kernel": {"us": round(k_us, 2), "Tkv": T, "allowed_keys": n_allowed,
+                          "bytes": k_bytes, "GBps": round(gbps, 1),
+                          "frac_of_hbm_peak": round(gbps / PEAK_HBM_GBS, 3)},
+    }))
+
+
 def backbone_step(args, dev):
     """one training step (mask creation from the device-resident
     span / link lists, embedding, 12 layers, RMSNorm, tied linear + CE loss,
@@ -259,6 +384,9 @@ def main():
     ap.add_argument("--cpu-threads", type=int, default=min(16, os.cpu_count() or 1))
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device copy (HBM-counter calibration)")
+    ap.add_argument("--decode", action="store_true",
+                    help="generation with the key/value cache on the configs[4] model "
+                         "(per-token latency, cached vs full recompute, decode kernel roofline)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -270,6 +398,9 @@ def main():
         sys.exit(2)
     dev = torch.device("cuda:0")
 
+    if args.decode:
+        decode_bench(args, dev)
+        return
     if args.config == 5:
         backbone_step(args, dev)
         return

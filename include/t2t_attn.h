@@ -222,6 +222,35 @@ int t2t_qkv_rope_backward(const t2t_tensor *dq, const t2t_tensor *dk, const t2t_
                           int32_t B, int32_t T, int32_t H, int32_t D, void *dqkv,
                           int64_t dqkv_sb, int64_t dqkv_st, void *stream);
 
+/*
+ * Decode step: attention of Tq new query rows per batch row against a
+ * key/value cache, for generation with cached keys and values.  Replaces the
+ * per-token full recompute of TS2TSModel.forward_inference
+ * (model/model.py:214-237) driven by the generation loop
+ * (model/generation_loop.py:90-92), whose last rows are the only ones used.
+ *   q        [B, Hq, Tq, D] new query rows (rotated), o [B, Hq, Tq, D] out,
+ *            lse2 float[B][Hq][Tq] out (log2 domain, as t2t_attn_fwd).
+ *   k, v     [B, Hkv, cap, D] caches; positions 0 .. Tkv - 1 are read.
+ *   key_doc  int32[Bm][key_stride], key_bits uint64[Bm][words][key_stride]:
+ *            per cached position its doc id and kv words.
+ *   q_pos    int32[Bm][Tq] absolute positions of the new rows, q_doc
+ *            int32[Bm][Tq], q_bits uint64[Bm][words][Tq].
+ *   Key j is allowed for new row t iff j <= q_pos[t] and (key_doc[j] ==
+ *   q_doc[t] or q_bits[.][t] & key_bits[.][j] != 0 in some word) -- the
+ *   doc_causal / cross_doc_link mask_mod.
+ *   workspace: float[t2t_attn_decode_workspace(B, Hq, Tq, Tkv, D) / 4].
+ * Supported: bf16, D in {64, 128}, (Hq / Hkv) * Tq <= 8, words <= 8.
+ */
+int64_t t2t_attn_decode_workspace(int32_t B, int32_t Hq, int32_t Tq, int32_t Tkv, int32_t D);
+
+int t2t_attn_decode(const t2t_tensor *q, const t2t_tensor *k, const t2t_tensor *v,
+                    const t2t_tensor *o, float *lse2, const int32_t *key_doc,
+                    const uint64_t *key_bits, int64_t key_stride, const int32_t *q_pos,
+                    const int32_t *q_doc, const uint64_t *q_bits, int32_t mask_batch,
+                    int32_t words, int32_t B, int32_t Hq, int32_t Hkv, int32_t Tq, int32_t Tkv,
+                    int32_t D, int32_t dtype, float scale, void *workspace,
+                    int64_t workspace_bytes, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

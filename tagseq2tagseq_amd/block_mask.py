@@ -130,6 +130,39 @@ def _as_words(bits: Optional[torch.Tensor], Bm: int, T: int, device) -> torch.Te
     return bits.to(device=device).view(torch.int64).contiguous()
 
 
+@dataclass
+class MaskInputs:
+    """The per-token inputs of a mask without its tile tables: what the
+    decode-step kernel reads (doc ids and q / kv words per position)."""
+    seq_len: int
+    doc_ids: torch.Tensor          # int32 [Bm, T]
+    q_bits: torch.Tensor           # int64 [Bm, W, T]
+    kv_bits: torch.Tensor          # int64 [Bm, W, T]
+
+    @property
+    def mask_batch(self) -> int:
+        return int(self.doc_ids.shape[0])
+
+    @property
+    def words(self) -> int:
+        return int(self.q_bits.shape[1])
+
+
+def mask_inputs(doc_ids: torch.Tensor, q_bits: Optional[torch.Tensor] = None,
+                kv_bits: Optional[torch.Tensor] = None) -> MaskInputs:
+    """The inputs build_block_mask takes, normalised to [Bm, T] / [Bm, W, T]."""
+    if doc_ids.dim() == 1:
+        doc_ids = doc_ids.unsqueeze(0)
+    doc_ids = doc_ids.to(torch.int32).contiguous()
+    Bm, T = doc_ids.shape
+    qb = _as_words(q_bits, Bm, T, doc_ids.device)
+    kb = _as_words(kv_bits, Bm, T, doc_ids.device)
+    if qb.shape != kb.shape or qb.shape[0] != Bm or qb.shape[2] != T:
+        raise ValueError(f"q_bits {tuple(qb.shape)} / kv_bits {tuple(kb.shape)} do not match "
+                         f"doc_ids {tuple(doc_ids.shape)}")
+    return MaskInputs(T, doc_ids, qb, kb)
+
+
 def build_block_mask(doc_ids: torch.Tensor, q_bits: Optional[torch.Tensor] = None,
                      kv_bits: Optional[torch.Tensor] = None,
                      stream: Optional[torch.cuda.Stream] = None) -> T2TBlockMask:

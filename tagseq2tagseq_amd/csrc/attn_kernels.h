@@ -92,4 +92,15 @@ hipError_t launch_qkv_rope_bwd(const TensorView& dq, const TensorView& dk, const
                                int pos0, __bf16* dqkv, int64_t sb, int64_t st,
                                hipStream_t stream);
 
+// Decode step: Tq new query rows per batch row against a key/value cache of
+// Tkv filled positions, mask evaluated per key from doc ids and words.
+constexpr int kDecodeMaxRows = 8;  // (Hq / Hkv) * Tq per launch
+int64_t decode_workspace_floats(int B, int Hq, int Tq, int Tkv, int D);
+hipError_t launch_attn_decode(const TensorView& q, const TensorView& k, const TensorView& v,
+                              const TensorView& o, float* lse2, const int32_t* key_doc,
+                              const uint64_t* key_bits, int64_t key_stride, const int32_t* q_pos,
+                              const int32_t* q_doc, const uint64_t* q_bits, int Bm, int W,
+                              int B, int Hq, int Hkv, int Tq, int Tkv, int D, float scale,
+                              float* workspace, hipStream_t stream);
+
 }  // namespace t2t

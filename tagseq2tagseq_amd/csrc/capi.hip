@@ -315,4 +315,47 @@ int t2t_qkv_rope_backward(const t2t_tensor* dq, const t2t_tensor* dk, const t2t_
                     "t2t_qkv_rope_backward launch");
 }
 
+int64_t t2t_attn_decode_workspace(int32_t B, int32_t Hq, int32_t Tq, int32_t Tkv, int32_t D) {
+  if (B < 0 || Hq < 0 || Tq < 0 || Tkv < 0 || D < 0) return 0;
+  return 4 * t2t::decode_workspace_floats(B, Hq, Tq, Tkv, D);
+}
+
+int t2t_attn_decode(const t2t_tensor* q, const t2t_tensor* k, const t2t_tensor* v,
+                    const t2t_tensor* o, float* lse2, const int32_t* key_doc,
+                    const uint64_t* key_bits, int64_t key_stride, const int32_t* q_pos,
+                    const int32_t* q_doc, const uint64_t* q_bits, int32_t mask_batch,
+                    int32_t words, int32_t B, int32_t Hq, int32_t Hkv, int32_t Tq, int32_t Tkv,
+                    int32_t D, int32_t dtype, float scale, void* workspace,
+                    int64_t workspace_bytes, void* stream) {
+  if (B < 0 || Hq < 0 || Hkv < 0 || Tq < 0 || Tkv < 0 || mask_batch < 0 || key_stride < 0)
+    return fail(T2T_EINVAL, "negative size or stride");
+  if (dtype != T2T_DTYPE_BF16) return fail(T2T_EUNSUPPORTED, "dtype %d is not bf16", dtype);
+  if (D != 64 && D != 128) return fail(T2T_EUNSUPPORTED, "head dim %d (64 or 128)", D);
+  if (words < 0 || words > T2T_MAX_WORDS)
+    return fail(T2T_EUNSUPPORTED, "words=%d outside [0, %d]", words, T2T_MAX_WORDS);
+  if (B == 0 || Hq == 0 || Tq == 0) return T2T_OK;
+  if (Hkv == 0 || Hq % Hkv != 0)
+    return fail(T2T_EINVAL, "Hq=%d is not a multiple of Hkv=%d", Hq, Hkv);
+  if ((int64_t)(Hq / Hkv) * Tq > t2t::kDecodeMaxRows)
+    return fail(T2T_EUNSUPPORTED, "(Hq / Hkv) * Tq = %lld query rows per kv head exceeds %d",
+                (long long)(Hq / Hkv) * Tq, t2t::kDecodeMaxRows);
+  if (!(mask_batch == 1 || mask_batch == B))
+    return fail(T2T_EINVAL, "mask_batch %d does not broadcast to B=%d", mask_batch, B);
+  if (key_stride < Tkv) return fail(T2T_EINVAL, "key_stride %lld < Tkv %d", (long long)key_stride, Tkv);
+  if (!rope_view_ok(q) || !rope_view_ok(k) || !rope_view_ok(v) || !rope_view_ok(o))
+    return fail(T2T_EINVAL, "q/k/v/o view invalid (NULL, misaligned or bad stride)");
+  if (!lse2 || !key_doc || !q_pos || !q_doc || (words > 0 && (!key_bits || !q_bits)))
+    return fail(T2T_EINVAL, "NULL pointer argument");
+  const int64_t need = t2t_attn_decode_workspace(B, Hq, Tq, Tkv, D);
+  if (!workspace || workspace_bytes < need)
+    return fail(T2T_EINVAL, "workspace of %lld bytes, %lld needed", (long long)workspace_bytes,
+                (long long)need);
+  return hip_status(t2t::launch_attn_decode(as_view(q), as_view(k), as_view(v), as_view(o), lse2,
+                                            key_doc, key_bits, key_stride, q_pos, q_doc, q_bits,
+                                            mask_batch, words, B, Hq, Hkv, Tq, Tkv, D, scale,
+                                            static_cast<float*>(workspace),
+                                            static_cast<hipStream_t>(stream)),
+                    "t2t_attn_decode launch");
+}
+
 }  // extern "C"

@@ -1,0 +1,321 @@
+"""Inference wrapper with the reference's ``TS2TSModel`` interface, plus a
+cached forward for generation.
+
+Mirrors (reference file:line):
+  * ``TS2TSModel.__init__`` / ``from_config`` / ``eval`` / ``train`` / ``to``
+    (model/model.py:17-211): backbone, embedding / LM-head weights (tied by
+    default), final norm, mask creator;
+  * ``forward_inference(tokens, doc_spans, **kwargs)`` (model/model.py:214-237):
+    mask, embedding, backbone, norm, LM head over the whole sequence.
+
+Added for generation: ``forward_inference_last`` returns the logits of the
+last position only -- the single row the generation loop reads
+(model/generation_loop.py:90-97) -- and reuses the keys / values of every
+position whose inputs are unchanged since the previous call (``KVCache``).
+The reusable prefix is the longest one over which the token ids and all mask
+inputs (doc id, q words, kv words) agree: a position's hidden states depend
+only on the positions before it and on its own mask row, so they are exact
+for that prefix.  New rows go through each layer with the decode-step kernel
+(``t2t_attn_decode``, up to 8 rows per kv head per launch); when more than
+``prefill_rows`` rows are new, the whole sequence is recomputed through the
+block-mask kernels and the cache refilled.
+"""
+from __future__ import annotations
+
+from typing import Any, Callable, List, Optional
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from .attention import flex_attention
+from .block_mask import T2TBlockMask, build_block_mask
+from .decode import MAX_ROWS, attn_decode
+from .modules import RMSNorm, TS2TSBackbone
+from .rope import qkv_rope
+
+
+class KVCache:
+    """Keys and values of every layer for the cached positions of one
+    sequence (batch 1), with the token ids and mask inputs they were computed
+    under.  Storage: k, v bf16 [L][1][H][cap][D]; doc int32 [1][cap]; q / kv
+    words int64 [1][W][cap]."""
+
+    def __init__(self, num_layers: int, num_heads: int, head_dim: int, capacity: int,
+                 words: int, device, dtype=torch.bfloat16):
+        shape = (num_layers, 1, num_heads, capacity, head_dim)
+        self.k = torch.empty(shape, dtype=dtype, device=device)
+        self.v = torch.empty(shape, dtype=dtype, device=device)
+        self.tokens = torch.full((1, capacity), -1, dtype=torch.int64, device=device)
+        self.doc = torch.empty((1, capacity), dtype=torch.int32, device=device)
+        self.q_bits = torch.zeros((1, words, capacity), dtype=torch.int64, device=device)
+        self.kv_bits = torch.zeros((1, words, capacity), dtype=torch.int64, device=device)
+        self.capacity = capacity
+        self.words = words
+        self.length = 0
+
+    def reusable_prefix(self, tokens: torch.Tensor, bm) -> int:
+        """Length of the longest prefix whose token ids and mask inputs match."""
+        n = min(self.length, tokens.shape[1])
+        if n == 0:
+            return 0
+        diff = (self.tokens[0, :n] != tokens[0, :n]) | (self.doc[0, :n] != bm.doc_ids[0, :n])
+        if self.words:
+            diff |= (self.q_bits[0, :, :n] != bm.q_bits[0, :, :n]).any(0)
+            diff |= (self.kv_bits[0, :, :n] != bm.kv_bits[0, :, :n]).any(0)
+        idx = torch.nonzero(diff)
+        return int(idx[0, 0]) if idx.numel() else n
+
+    def store_inputs(self, tokens: torch.Tensor, bm, p0: int, p1: int) -> None:
+        self.tokens[0, p0:p1] = tokens[0, p0:p1]
+        self.doc[0, p0:p1] = bm.doc_ids[0, p0:p1]
+        if self.words:
+            self.q_bits[0, :, p0:p1] = bm.q_bits[0, :, p0:p1]
+            self.kv_bits[0, :, p0:p1] = bm.kv_bits[0, :, p0:p1]
+
+
+class TS2TSModel:
+    """model/model.py:17-237 (generation / evaluation helpers that need the
+    absent tokenizer stack are not provided)."""
+
+    def __init__(self, backbone: TS2TSBackbone, embedding_weight: torch.Tensor,
+                 lm_head_weight: torch.Tensor, norm: nn.Module, block_mask_creator: Callable,
+                 vocab_size: int, ignore_index: int = -100, tokenizer=None, link_detector=None,
+                 layout_policy=None):
+        self.backbone = backbone
+        self.embedding_weight = embedding_weight
+        self.lm_head_weight = lm_head_weight
+        self.norm = norm
+        self.block_mask_creator = block_mask_creator
+        self.vocab_size = vocab_size
+        self.ignore_index = ignore_index
+        self.tokenizer = tokenizer
+        self.link_detector = link_detector
+        self.layout_policy = layout_policy
+        self.kv_cache: Optional[KVCache] = None
+        self.prefill_rows = 64
+        self.use_graphs = True
+        self._graph: Optional[_DecodeGraph] = None
+
+    @classmethod
+    def from_config(cls, vocab_size: int, num_layers: int, model_dim: int, num_heads: int,
+                    max_seq_len: int, dropout: float, drop_path_rate: float,
+                    block_mask_creator: Callable, fp8: bool = False, weight_tying: bool = True,
+                    ignore_index: int = -100, tokenizer=None, link_detector=None,
+                    layout_policy=None) -> "TS2TSModel":
+        backbone = TS2TSBackbone(num_layers=num_layers, model_dim=model_dim, num_heads=num_heads,
+                                 max_seq_len=max_seq_len, dropout=dropout,
+                                 drop_path_rate=drop_path_rate, fp8=fp8)
+        embedding = nn.Embedding(vocab_size, model_dim)
+        norm = RMSNorm(model_dim)
+        if weight_tying:
+            lm_head_weight = embedding.weight
+        else:
+            lm_head_weight = nn.Parameter(torch.empty(vocab_size, model_dim))
+            nn.init.normal_(lm_head_weight, mean=0.0, std=0.02)
+        return cls(backbone, embedding.weight, lm_head_weight, norm, block_mask_creator,
+                   vocab_size, ignore_index, tokenizer, link_detector, layout_policy)
+
+    def eval(self):
+        self.backbone.eval()
+        return self
+
+    def train(self, mode: bool = True):
+        self.backbone.train(mode)
+        return self
+
+    def to(self, device, dtype=None):
+        self.backbone.to(device, dtype)
+        self.norm.to(device, dtype)
+        tied = self.lm_head_weight is self.embedding_weight
+        self.embedding_weight = self.embedding_weight.to(device=device, dtype=dtype)
+        self.lm_head_weight = (self.embedding_weight if tied else
+                               self.lm_head_weight.to(device=device, dtype=dtype))
+        self.kv_cache = None
+        self._graph = None
+        return self
+
+    def reset_cache(self) -> None:
+        self.kv_cache = None
+        self._graph = None
+
+    @torch.no_grad()
+    def forward_inference(self, tokens: torch.Tensor, doc_spans: Optional[List[Any]] = None,
+                          **kwargs) -> torch.Tensor:
+        """model/model.py:214-237: logits [1, T, V] over the whole sequence."""
+        block_mask = self.block_mask_creator(tokens=tokens, doc_spans=doc_spans or [], **kwargs)
+        x = F.embedding(tokens, self.embedding_weight)
+        x = self.backbone(x, block_mask=block_mask)
+        x = self.norm(x)
+        return F.linear(x, self.lm_head_weight)
+
+    # -- cached path -------------------------------------------------------
+
+    def _layers(self):
+        return self.backbone.layers
+
+    def _new_cache(self, words: int, device) -> KVCache:
+        attn = self._layers()[0].attn
+        return KVCache(len(self._layers()), attn.num_heads, attn.head_dim,
+                       self._layers()[0].attn.rotary.max_seq_len, words, device,
+                       self.embedding_weight.dtype)
+
+    @torch.no_grad()
+    def forward_inference_last(self, tokens: torch.Tensor,
+                               doc_spans: Optional[List[Any]] = None, **kwargs) -> torch.Tensor:
+        """Logits [1, 1, V] of the last position of ``tokens`` [1, T]; equal
+        (to bf16 rounding) to ``forward_inference(tokens, doc_spans)[:, -1:]``."""
+        if tokens.shape[0] != 1:
+            raise ValueError("the cached path serves one sequence (batch 1)")
+        # Per-token mask inputs only; the tile tables are built below if the
+        # whole sequence has to be recomputed.
+        bm = self.block_mask_creator(tokens=tokens, doc_spans=doc_spans or [], inputs_only=True,
+                                     **kwargs)
+        T = tokens.shape[1]
+        cache = self.kv_cache
+        if cache is None or cache.words != bm.words or T > cache.capacity:
+            cache = self.kv_cache = self._new_cache(bm.words, tokens.device)
+            self._graph = None
+        p0 = min(cache.reusable_prefix(tokens, bm), T - 1)
+        full = T - p0 > self.prefill_rows
+        if full:
+            p0 = 0
+            if not isinstance(bm, T2TBlockMask):
+                bm = build_block_mask(bm.doc_ids, bm.q_bits, bm.kv_bits)
+        cache.length = p0  # positions >= p0 are rewritten below
+        cache.store_inputs(tokens, bm, p0, T)
+        if self.use_graphs and not full and T - p0 == 1:
+            logits = self._graph_step(cache, tokens, bm, p0)
+            cache.length = T
+            return logits
+        x = F.embedding(tokens[:, p0:], self.embedding_weight)
+        x = self._backbone_rows(x, bm, cache, p0, full)
+        cache.length = T
+        x = self.norm(x[:, -1:])
+        return F.linear(x, self.lm_head_weight)
+
+    def _graph_step(self, cache: KVCache, tokens: torch.Tensor, bm, p: int) -> torch.Tensor:
+        """One new row at position p through the captured decode step."""
+        if self._graph is None or self._graph.cache is not cache:
+            self._graph = _DecodeGraph(self, cache)
+        return self._graph.run(tokens, bm, p)
+
+    def _step_body(self, cache: KVCache, buf: "_DecodeGraph") -> torch.Tensor:
+        """The single-row step over static buffers (no host values in any
+        launch): embedding, every layer with its cache write and decode
+        attention over the whole cache capacity (slots past the new row are
+        excluded by the causal test), final norm and LM head."""
+        x = F.embedding(buf.tok, self.embedding_weight)
+        cos_t, sin_t = self._layers()[0].attn.rotary.tables(x.device)
+        cos = cos_t.index_select(0, buf.pos)
+        sin = sin_t.index_select(0, buf.pos)
+        bb = self.backbone
+        skips = []
+        n_skip = len(bb.skip_weights)
+        for i, layer in enumerate(bb.layers):
+            if i >= n_skip and skips:
+                x = x + bb.skip_weights[i - n_skip] * skips.pop()
+            attn = layer.attn
+            C = x.shape[-1]
+            q, k, v = qkv_rope(attn.qkv(layer.ln_1(x)), cos, sin, attn.num_heads, 0)
+            cache.k[i].index_copy_(2, buf.pos, k)
+            cache.v[i].index_copy_(2, buf.pos, v)
+            y, _ = attn_decode(q, cache.k[i], cache.v[i], cache.capacity, cache.doc,
+                               cache.kv_bits if cache.words else None, buf.qpos, buf.qdoc,
+                               buf.qbits)
+            y = attn.proj(y.transpose(1, 2).reshape(1, 1, C))
+            x = x + layer.drop_path(y)
+            x = x + layer.drop_path(layer.mlp(layer.ln_2(x)))
+            if i < n_skip:
+                skips.append(x)
+        return F.linear(self.norm(x), self.lm_head_weight)
+
+    def _backbone_rows(self, x, bm, cache: KVCache, p0: int, full: bool):
+        """TS2TSBackbone.forward (skip wiring of model/modules/backbone.py:93-104)
+        over rows p0 .. T - 1 with cached attention."""
+        bb = self.backbone
+        skips = []
+        n_skip = len(bb.skip_weights)
+        for i, layer in enumerate(bb.layers):
+            if i >= n_skip and skips:
+                x = x + bb.skip_weights[i - n_skip] * skips.pop()
+            x = self._layer_rows(i, layer, x, bm, cache, p0, full)
+            if i < n_skip:
+                skips.append(x)
+        return x
+
+    def _layer_rows(self, i: int, layer, x, bm, cache: KVCache, p0: int, full: bool):
+        """Layer.forward (model/modules/layer.py:32-35) over the new rows."""
+        attn = layer.attn
+        B, n, C = x.shape
+        T = p0 + n
+        cos, sin = attn.rotary.tables(x.device)
+        q, k, v = qkv_rope(attn.qkv(layer.ln_1(x)), cos, sin, attn.num_heads, p0)
+        cache.k[i, :, :, p0:T] = k
+        cache.v[i, :, :, p0:T] = v
+        if full:
+            y = flex_attention(q, k, v, block_mask=bm)
+        else:
+            y = torch.empty_like(q)
+            rows = MAX_ROWS  # one query head per kv head in this model
+            pos = torch.arange(p0, T, dtype=torch.int32, device=x.device)[None]
+            for c0 in range(0, n, rows):
+                c1 = min(n, c0 + rows)
+                qb = bm.q_bits[:, :, p0 + c0:p0 + c1].contiguous() if bm.words else None
+                attn_decode(q[:, :, c0:c1], cache.k[i], cache.v[i], p0 + c1, cache.doc,
+                            cache.kv_bits if bm.words else None, pos[:, c0:c1].contiguous(),
+                            bm.doc_ids[:, p0 + c0:p0 + c1].contiguous(), qb,
+                            out=y[:, :, c0:c1])
+        y = attn.proj(y.transpose(1, 2).reshape(B, n, C))
+        x = x + layer.drop_path(y)
+        return x + layer.drop_path(layer.mlp(layer.ln_2(x)))
+
+
+class _DecodeGraph:
+    """The single-row decode step of a TS2TSModel captured as a HIP graph
+    (torch.cuda.graph) over static buffers: token id, position (int64 for
+    index_select / index_copy_, int32 for the decode kernel) and the new
+    row's doc id and q words.  Replays cost one launch from the host instead
+    of the ~30 launches per layer of the eager step; the recorded kernels
+    (hipBLASLt GEMMs, torch elementwise / reduction kernels, the prologue and
+    decode kernels) write no memset nodes of their own."""
+
+    def __init__(self, model: TS2TSModel, cache: KVCache):
+        dev = cache.k.device
+        self.cache = cache
+        self.tok = torch.zeros((1, 1), dtype=torch.int64, device=dev)
+        self.pos = torch.zeros((1,), dtype=torch.int64, device=dev)
+        self.qpos = torch.zeros((1, 1), dtype=torch.int32, device=dev)
+        self.qdoc = torch.zeros((1, 1), dtype=torch.int32, device=dev)
+        self.qbits = (torch.zeros((1, cache.words, 1), dtype=torch.int64, device=dev)
+                      if cache.words else None)
+        self.model = model
+        self.graph = None
+        self.logits = None
+
+    def _capture(self):
+        """Warm up on a side stream (default priority), then capture.  The
+        buffers already hold the first step's values, so the warm-up run writes
+        exactly what the first replay writes."""
+        dev = self.tok.device
+        side = torch.cuda.Stream(device=dev)
+        side.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(side):
+            self.model._step_body(self.cache, self)
+        torch.cuda.current_stream(dev).wait_stream(side)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self.logits = self.model._step_body(self.cache, self)
+
+    def run(self, tokens: torch.Tensor, bm, p: int) -> torch.Tensor:
+        self.tok.copy_(tokens[:, p:p + 1])
+        self.pos.fill_(p)
+        self.qpos.fill_(p)
+        self.qdoc.copy_(bm.doc_ids[:, p:p + 1])
+        if self.qbits is not None:
+            self.qbits.copy_(bm.q_bits[:, :, p:p + 1])
+        if self.graph is None:
+            self._capture()
+        self.graph.replay()
+        return self.logits.clone()
+

@@ -1,0 +1,193 @@
+"""GPU parity of the decode step (t2t_attn_decode) and of the cached
+generation forward built on it.
+
+Kernel: the rows of the float64 oracle attention (oracle/attn_oracle.py, the
+restatement of torch's math attention under the reference mask_mod) at the
+new rows' positions, bf16 tolerance 2e-2 abs+rel on o and 1e-3 on the LSE;
+GQA, per-row masks, grant words, uncovered tokens, ragged key counts, cache
+slots past the filled length holding NaN (never read), fully masked rows.
+Model: TS2TSModel.forward_inference_last against the last row of the full
+recompute forward_inference (the reference's per-token path) while tokens are
+appended one and several at a time, after an early token changes, and under a
+cross-document link mask.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attn_oracle as ao
+from oracle import mask_oracle as mo
+from tagseq2tagseq_amd import synth
+from tagseq2tagseq_amd.decode import attn_decode
+from tagseq2tagseq_amd.mask_creators import (create_doc_causal_block_mask,
+                                             create_doc_link_block_mask)
+from tagseq2tagseq_amd.model import TS2TSModel
+from tests.helpers import assert_close, random_row, to_dev_words
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda:0")
+LOG2E = 1.0 / math.log(2.0)
+
+
+def _decode_case(rows_np, B, Hq, Hkv, T, D, Tq, cap, seed, positions=None):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(B, Hq, T, D, generator=g).to(torch.bfloat16)
+    k = torch.randn(B, Hkv, T, D, generator=g).to(torch.bfloat16)
+    v = torch.randn(B, Hkv, T, D, generator=g).to(torch.bfloat16)
+    pos = np.arange(T - Tq, T) if positions is None else np.asarray(positions)
+    # caches with NaN past the filled length
+    kc = torch.full((B, Hkv, cap, D), float("nan"), dtype=torch.bfloat16)
+    vc = torch.full((B, Hkv, cap, D), float("nan"), dtype=torch.bfloat16)
+    kc[:, :, :T] = k
+    vc[:, :, :T] = v
+    Bm = len(rows_np)
+    W = 0 if rows_np[0][1] is None else rows_np[0][1].shape[0]
+    key_doc = torch.full((Bm, cap), -7, dtype=torch.int32)
+    key_doc[:, :T] = torch.from_numpy(np.stack([r[0] for r in rows_np]))
+    key_bits = q_bits = None
+    if W:
+        key_bits = torch.zeros((Bm, W, cap), dtype=torch.int64)
+        key_bits[:, :, :T] = torch.stack([to_dev_words(r[2], "cpu") for r in rows_np])
+        q_bits = torch.stack([to_dev_words(r[1][:, pos], "cpu") for r in rows_np])
+    q_doc = torch.from_numpy(np.stack([r[0][pos] for r in rows_np])).int()
+    q_pos = torch.from_numpy(np.tile(pos.astype(np.int32), (Bm, 1)))
+    dev = lambda t: None if t is None else t.to(DEV).contiguous()
+    o, lse2 = attn_decode(dev(q[:, :, pos]), dev(kc), dev(vc), T, dev(key_doc), dev(key_bits),
+                          dev(q_pos), dev(q_doc), dev(q_bits))
+    dense = np.stack([mo.dense_mask(*r) for r in rows_np])
+    o_ref, lse_ref = ao.attention_fwd(q.float().numpy(), k.float().numpy(), v.float().numpy(),
+                                      dense)
+    label = f"B{B} H{Hq}/{Hkv} T{T} D{D} Tq{Tq}"
+    assert_close(o, torch.from_numpy(o_ref[:, :, pos]), 2e-2, 2e-2, f"o {label}")
+    assert_close(lse2, torch.from_numpy(lse_ref[:, :, pos] * LOG2E), 1e-3, 1e-3, f"lse {label}")
+    return o, lse2
+
+
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("T", [1, 200, 1000, 4099])
+def test_single_row_doc_causal(T, D):
+    rows = [random_row(T, np.random.default_rng(T + D), max_doc=600)]
+    _decode_case(rows, 1, 2, 2, T, D, 1, T + 37, seed=T)
+
+
+@pytest.mark.parametrize("D", [64, 128])
+def test_gqa_rows_words_and_batch_masks(D):
+    """R = (Hq / Hkv) * Tq = 8 rows per kv head; per-row masks with 2 words."""
+    rng = np.random.default_rng(21)
+    T = 777
+    rows = [random_row(T, rng, words=2, uncovered=True, max_doc=150) for _ in range(2)]
+    _decode_case(rows, 2, 8, 2, T, D, 2, 1024, seed=3)
+
+
+def test_rows_at_arbitrary_positions():
+    rng = np.random.default_rng(5)
+    T = 600
+    rows = [random_row(T, rng, words=1, max_doc=100)]
+    _decode_case(rows, 1, 4, 4, T, 128, 2, 640, seed=4, positions=[17, 402])
+
+
+def test_cross_doc_link_rows():
+    row = synth.config_rows(3, seed=1, T=2048)[0]
+    doc = mo.document_ids(2048, row.spans)
+    qb, kb = mo.doc_link_token_bits(row.doc_index, row.link_rows)
+    _decode_case([(doc, qb, kb)], 1, 4, 4, 2048, 128, 2, 2048, seed=6)
+
+
+def test_fully_masked_row():
+    T, D = 300, 64
+    kc = torch.randn(1, 1, T, D, device=DEV).to(torch.bfloat16)
+    key_doc = torch.zeros(1, T, dtype=torch.int32, device=DEV)
+    q = torch.randn(1, 1, 1, D, device=DEV).to(torch.bfloat16)
+    o, lse2 = attn_decode(q, kc, kc, T, key_doc, None,
+                          torch.tensor([[T - 1]], dtype=torch.int32, device=DEV),
+                          torch.tensor([[5]], dtype=torch.int32, device=DEV), None)
+    assert torch.equal(o.float(), torch.zeros_like(o.float()))
+    assert torch.isneginf(lse2).all()
+
+
+def test_too_many_rows_raises():
+    q = torch.zeros(1, 4, 3, 64, dtype=torch.bfloat16, device=DEV)
+    kc = torch.zeros(1, 1, 16, 64, dtype=torch.bfloat16, device=DEV)
+    i32 = torch.zeros(1, 16, dtype=torch.int32, device=DEV)
+    with pytest.raises(RuntimeError, match="exceeds"):
+        attn_decode(q, kc, kc, 16, i32, None, i32[:, :3].contiguous(), i32[:, :3].contiguous(),
+                    None)
+
+
+# -- cached model path ------------------------------------------------------
+
+def _model(creator, T_max=1024):
+    torch.manual_seed(0)
+    m = TS2TSModel.from_config(vocab_size=500, num_layers=4, model_dim=256, num_heads=4,
+                               max_seq_len=T_max, dropout=0.0, drop_path_rate=0.0,
+                               block_mask_creator=creator)
+    with torch.no_grad():
+        m.embedding_weight.mul_(0.05)  # keeps logits in a range where bf16 rounding is small
+    return m.to(DEV, torch.bfloat16).eval()
+
+
+def _check_last(m, tokens, spans, what, **kw):
+    got = m.forward_inference_last(tokens, spans, **kw).float()
+    ref = m.forward_inference(tokens, spans, **kw)[:, -1:].float()
+    scale = ref.abs().max().item()
+    err = (got - ref).abs().max().item()
+    assert err <= 2e-2 * scale + 1e-3, f"{what}: max err {err:.4g} (logit scale {scale:.3g})"
+
+
+def _grow(spans, n):
+    """Extend the last document by n tokens."""
+    last = spans[-1]
+    return spans[:-1] + [synth.DocSpan(doc_id=last.doc_id, start=last.start, end=last.end + n)]
+
+
+@pytest.mark.parametrize("graphs", [True, False])
+def test_cached_generation_matches_full_recompute(graphs):
+    """Single-row steps run through the captured HIP graph (graphs=True, replayed
+    with eager work and host synchronisation between replays) or eagerly."""
+    m = _model(create_doc_causal_block_mask)
+    m.use_graphs = graphs
+    g = torch.Generator().manual_seed(1)
+    vocab = torch.randint(0, 500, (1, 1024), generator=g).to(DEV)
+    spans = [synth.DocSpan(doc_id=7, start=0, end=120), synth.DocSpan(doc_id=3, start=120, end=300)]
+    T = 300
+    _check_last(m, vocab[:, :T], spans, "prefill")
+    assert m.kv_cache.length == T
+    for step in range(8):  # one token at a time: decode path
+        spans = _grow(spans, 1)
+        T += 1
+        _check_last(m, vocab[:, :T], spans, f"decode step {step}")
+    spans = _grow(spans, 5)  # five new rows at once
+    T += 5
+    _check_last(m, vocab[:, :T], spans, "5-row step")
+    # an earlier token changes: rows from there on are recomputed (40 rows, decode chunks)
+    tok = vocab[:, :T].clone()
+    tok[0, T - 40] = (tok[0, T - 40] + 1) % 500
+    _check_last(m, tok, spans, "changed token")
+    # a new document appended after the generated one
+    spans2 = spans + [synth.DocSpan(doc_id=11, start=T, end=T + 3)]
+    _check_last(m, torch.cat([tok, vocab[:, T:T + 3]], 1), spans2, "new doc")
+
+
+@pytest.mark.parametrize("graphs", [True, False])
+def test_cached_generation_cross_doc_links(graphs):
+    m = _model(create_doc_link_block_mask)
+    m.use_graphs = graphs
+    g = torch.Generator().manual_seed(2)
+    vocab = torch.randint(0, 500, (1, 1024), generator=g).to(DEV)
+    spans = [synth.DocSpan(doc_id=i, start=100 * i, end=100 * i + 100) for i in range(4)]
+    links = np.zeros((4, 1), dtype=np.uint64)
+    for i in range(4):
+        links[i, 0] |= np.uint64(1) << np.uint64(i)
+    links[3, 0] |= np.uint64(1 << 1)
+    T = 400
+    _check_last(m, vocab[:, :T], spans, "prefill", doc_links=links)
+    for step in range(3):
+        spans = _grow(spans, 1)
+        T += 1
+        _check_last(m, vocab[:, :T], spans, f"decode {step}", doc_links=links)
+    links2 = links.copy()
+    links2[3, 0] |= np.uint64(1)  # the generated doc gains a link: its rows change
+    _check_last(m, vocab[:, :T], spans, "link added", doc_links=links2)

@@ -158,3 +158,30 @@ def test_qkv_rope_argument_checks():
     assert lib.t2t_qkv_rope_backward(v, v, None, P, P, 32, 0, 1, 32, 4, 64, P, 0, 768,
                                      None) == -1
     assert "view" in _err()
+
+
+def test_attn_decode_argument_checks():
+    lib = _lib.lib()
+    P = ctypes.c_void_p(0x1000)
+    view = _lib.T2TTensor(0x1000, 0, 64 * 128, 64)
+    v = ctypes.byref(view)
+    ws = lib.t2t_attn_decode_workspace(1, 4, 1, 1000, 64)
+    assert ws == 4 * 1 * 4 * 1 * 4 * (64 + 2)  # ceil(1000 / 256) chunks of (D + 2) floats
+
+    def call(**kw):
+        a = dict(q=v, k=v, v=v, o=v, lse2=P, key_doc=P, key_bits=None, key_stride=1000, q_pos=P,
+                 q_doc=P, q_bits=None, mask_batch=1, words=0, B=1, Hq=4, Hkv=4, Tq=1,
+                 Tkv=1000, D=64, dtype=0, scale=0.125, ws=P, ws_bytes=ws, stream=None)
+        a.update(kw)
+        return lib.t2t_attn_decode(*a.values())
+
+    assert call(Tq=0) == 0  # no rows: no-op
+    assert call(D=96) == -2 and "head dim" in _err()
+    assert call(dtype=1) == -2
+    assert call(Hq=6) == -1 and "multiple" in _err()
+    assert call(Hq=8, Hkv=1, Tq=2) == -2 and "exceeds" in _err()
+    assert call(mask_batch=2) == -1 and "broadcast" in _err()
+    assert call(key_stride=999) == -1 and "key_stride" in _err()
+    assert call(words=1) == -1 and "NULL" in _err()
+    assert call(ws_bytes=ws - 4) == -1 and "workspace" in _err()
+    assert call(words=9) == -2
