@@ -251,6 +251,33 @@ int t2t_attn_decode(const t2t_tensor *q, const t2t_tensor *k, const t2t_tensor *
                     int32_t D, int32_t dtype, float scale, void *workspace,
                     int64_t workspace_bytes, void *stream);
 
+/*
+ * RMS normalisation of token rows: y = x / sqrt(mean(x^2) + eps) * weight in
+ * fp32, rounded once to bf16.  Replaces the RMSNorm modules of the reference's
+ * layers and head (model/modules/layer.py:14,19; training_module.py:122-123;
+ * tunalab's RMSNorm, not part of the reference).
+ *   x, y     bf16 rows [N][C] with row strides (elements); C % 8 == 0, C <= 4096.
+ *   weight   [C], weight_dtype 0 = bf16, 1 = float32.
+ *   rstd     float[N] out: 1 / rms per row (input of the backward).
+ */
+int t2t_rms_norm(const void *x, int64_t x_stride, const void *weight, int32_t weight_dtype,
+                 void *y, int64_t y_stride, float *rstd, int32_t N, int32_t C, float eps,
+                 void *stream);
+
+/* Workspace (bytes) of t2t_rms_norm_backward for N rows of C. */
+int64_t t2t_rms_norm_backward_workspace(int32_t N, int32_t C);
+
+/*
+ * Gradient of t2t_rms_norm: dx = r (g - xh mean(g xh)) with r = rstd,
+ * xh = x r, g = dy weight; dweight = sum over rows of dy xh (weight dtype),
+ * reduced in a fixed order (deterministic, no atomics).  dx and dweight are
+ * written, not accumulated.
+ */
+int t2t_rms_norm_backward(const void *dy, int64_t dy_stride, const void *x, int64_t x_stride,
+                          const void *weight, int32_t weight_dtype, const float *rstd, void *dx,
+                          int64_t dx_stride, void *dweight, void *workspace,
+                          int64_t workspace_bytes, int32_t N, int32_t C, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

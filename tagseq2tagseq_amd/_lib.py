@@ -55,6 +55,11 @@ _SIGS = {
                      ctypes.c_int),
     "t2t_qkv_rope_backward": ([_P] * 5 + [_I32] * 6 + [_P, _I64, _I64, _P], ctypes.c_int),
     "t2t_attn_decode_workspace": ([_I32] * 5, ctypes.c_int64),
+    "t2t_rms_norm": ([_P, _I64, _P, _I32, _P, _I64, _P, _I32, _I32, ctypes.c_float, _P],
+                     ctypes.c_int),
+    "t2t_rms_norm_backward_workspace": ([_I32, _I32], ctypes.c_int64),
+    "t2t_rms_norm_backward": ([_P, _I64, _P, _I64, _P, _I32, _P, _P, _I64, _P, _P, _I64, _I32,
+                               _I32, _P], ctypes.c_int),
     "t2t_attn_decode": ([_P] * 7 + [_I64] + [_P] * 3 + [_I32] * 9 + [ctypes.c_float, _P, _I64, _P],
                         ctypes.c_int),
 }

@@ -6,12 +6,16 @@ Seams replaced (reference file:line):
     the module-global symbol the reference's attention module calls
     (model/modules/layer.py:16-21,33; monkey-patched at generate.py:167-178),
     i.e. torch/nn/attention/flex_attention.py:1396-1676.
-  * ``torch.ops.t2t.masked_attention`` -- in place of FlexAttentionAutogradOp
-    (torch/_higher_order_ops/flex_attention.py:628-767): a ``torch.library``
-    custom op (fake implementation + registered autograd, so compiled models
-    trace it) that saves q, k, v, out and the log2-domain LSE; its backward is
-    the custom op ``t2t::masked_attention_backward`` (atomic-free dK/dV + dQ
-    kernels).  ``T2TFlexAttentionFn`` is the same as a plain autograd.Function.
+  * FlexAttentionAutogradOp (torch/_higher_order_ops/flex_attention.py:628-767)
+    -- twice, over the same kernels: ``T2TFlexAttentionFn``, a plain
+    autograd.Function that eager calls use (saves q, k, v, out and the
+    log2-domain LSE; backward = atomic-free dK/dV + dQ kernels), and
+    ``torch.ops.t2t.masked_attention`` / ``t2t::masked_attention_backward``,
+    ``torch.library`` custom ops with fake implementations and registered
+    autograd that compiled graphs trace.  ``flex_attention`` picks the custom
+    op while torch.compile traces and the Function otherwise: the custom op's
+    registered autograd costs several hundred microseconds of host time per
+    call, the Function tens.
   * ``FlexSelfAttention(dim, num_heads, max_seq_len, fp8_out_proj)`` with
     ``forward(x, block_mask)`` -- the constructor / call signature the
     reference's Layer uses (model/modules/layer.py:16-21,33).
@@ -265,7 +269,13 @@ def flex_attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
     _, _, _, _, D = _validate(query, key, value, block_mask, enable_gqa)
     if scale is None:
         scale = 1.0 / math.sqrt(D)  # torch/nn/attention/flex_attention.py:1544
-    out, lse2 = masked_attention(query, key, value, block_mask.tables(), float(scale))
+    if torch.compiler.is_compiling():
+        # compiled graphs trace the custom op (schema + fake implementation)
+        out, lse2 = masked_attention(query, key, value, block_mask.tables(), float(scale))
+    else:
+        # eager: the same kernels through a plain autograd.Function, whose host
+        # cost per call is a fraction of the custom op's registered autograd
+        out, lse2 = T2TFlexAttentionFn.apply(query, key, value, block_mask, float(scale))
     if return_lse:
         return out, lse2 * LN2
     return out

@@ -103,4 +103,14 @@ hipError_t launch_attn_decode(const TensorView& q, const TensorView& k, const Te
                               int B, int Hq, int Hkv, int Tq, int Tkv, int D, float scale,
                               float* workspace, hipStream_t stream);
 
+// RMS normalisation of token rows (bf16 rows, bf16 or fp32 weight).
+int rmsnorm_bwd_groups(int N, int C);
+hipError_t launch_rmsnorm_fwd(const __bf16* x, int64_t xs, const void* w, bool w_f32, __bf16* y,
+                              int64_t ys, float* rstd, int N, int C, float eps,
+                              hipStream_t stream);
+hipError_t launch_rmsnorm_bwd(const __bf16* dy, int64_t dys, const __bf16* x, int64_t xs,
+                              const void* w, bool w_f32, const float* rstd, __bf16* dx,
+                              int64_t dxs, void* dw, float* part, int N, int C,
+                              hipStream_t stream);
+
 }  // namespace t2t

@@ -358,4 +358,69 @@ int t2t_attn_decode(const t2t_tensor* q, const t2t_tensor* k, const t2t_tensor* 
                     "t2t_attn_decode launch");
 }
 
+namespace {
+
+int check_norm(int N, int C, int wdt, const void* const* ptrs, int n_ptrs,
+               const int64_t* strides, int n_strides) {
+  if (N < 0 || C < 0) return fail(T2T_EINVAL, "negative N or C");
+  if (C % 8 != 0 || C > 4096 || C == 0)
+    return fail(T2T_EUNSUPPORTED, "row length %d is not a multiple of 8 in [8, 4096]", C);
+  if (wdt != 0 && wdt != 1) return fail(T2T_EUNSUPPORTED, "weight dtype %d (0 bf16, 1 f32)", wdt);
+  for (int i = 0; i < n_ptrs; ++i) {
+    if (!ptrs[i]) return fail(T2T_EINVAL, "NULL pointer argument");
+    if (reinterpret_cast<uintptr_t>(ptrs[i]) % 16)
+      return fail(T2T_EINVAL, "row, weight and gradient pointers must be 16-byte aligned");
+  }
+  for (int i = 0; i < n_strides; ++i)
+    if (strides[i] < C || strides[i] % 8)
+      return fail(T2T_EINVAL, "row stride %lld is below C or not a multiple of 8",
+                  (long long)strides[i]);
+  return T2T_OK;
+}
+
+}  // namespace
+
+int t2t_rms_norm(const void* x, int64_t x_stride, const void* weight, int32_t weight_dtype,
+                 void* y, int64_t y_stride, float* rstd, int32_t N, int32_t C, float eps,
+                 void* stream) {
+  if (N == 0 && C >= 0) return T2T_OK;
+  const void* ptrs[] = {x, weight, y};
+  const int64_t strides[] = {x_stride, y_stride};
+  int rc = check_norm(N, C, weight_dtype, ptrs, 3, strides, 2);
+  if (rc) return rc;
+  if (!rstd) return fail(T2T_EINVAL, "rstd is NULL");
+  return hip_status(t2t::launch_rmsnorm_fwd(static_cast<const __bf16*>(x), x_stride, weight,
+                                            weight_dtype == 1, static_cast<__bf16*>(y), y_stride,
+                                            rstd, N, C, eps, static_cast<hipStream_t>(stream)),
+                    "t2t_rms_norm launch");
+}
+
+int64_t t2t_rms_norm_backward_workspace(int32_t N, int32_t C) {
+  if (N <= 0 || C <= 0) return 0;
+  return (int64_t)t2t::rmsnorm_bwd_groups(N, C) * C * 4;
+}
+
+int t2t_rms_norm_backward(const void* dy, int64_t dy_stride, const void* x, int64_t x_stride,
+                          const void* weight, int32_t weight_dtype, const float* rstd, void* dx,
+                          int64_t dx_stride, void* dweight, void* workspace,
+                          int64_t workspace_bytes, int32_t N, int32_t C, void* stream) {
+  if (N == 0 && C >= 0) return T2T_OK;
+  const void* ptrs[] = {dy, x, weight, dx, dweight};
+  const int64_t strides[] = {dy_stride, x_stride, dx_stride};
+  int rc = check_norm(N, C, weight_dtype, ptrs, 5, strides, 3);
+  if (rc) return rc;
+  if (!rstd) return fail(T2T_EINVAL, "rstd is NULL");
+  const int64_t need = t2t_rms_norm_backward_workspace(N, C);
+  if (!workspace || workspace_bytes < need)
+    return fail(T2T_EINVAL, "workspace of %lld bytes, %lld needed", (long long)workspace_bytes,
+                (long long)need);
+  return hip_status(
+      t2t::launch_rmsnorm_bwd(static_cast<const __bf16*>(dy), dy_stride,
+                              static_cast<const __bf16*>(x), x_stride, weight, weight_dtype == 1,
+                              rstd, static_cast<__bf16*>(dx), dx_stride, dweight,
+                              static_cast<float*>(workspace), N, C,
+                              static_cast<hipStream_t>(stream)),
+      "t2t_rms_norm_backward launch");
+}
+
 }  // extern "C"

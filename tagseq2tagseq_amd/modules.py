@@ -27,11 +27,14 @@ import torch.nn as nn
 import torch.nn.functional as F
 import torch.utils.checkpoint
 
+from . import norm
 from .attention import FlexSelfAttention
 
 
 class RMSNorm(nn.Module):
-    """y = x / sqrt(mean(x^2) + eps) * weight (computed in fp32)."""
+    """y = x / sqrt(mean(x^2) + eps) * weight (computed in fp32).  bf16 rows on
+    the GPU run the one-pass kernels (t2t::rms_norm, with its gradient); other
+    dtypes and CPU tensors use the same formula in torch."""
 
     def __init__(self, dim: int, eps: float = 1e-6):
         super().__init__()
@@ -39,6 +42,8 @@ class RMSNorm(nn.Module):
         self.weight = nn.Parameter(torch.ones(dim))
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if norm.kernel_applies(x, self.weight):
+            return norm.rms_norm(x, self.weight, self.eps)
         xf = x.float()
         y = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + self.eps)
         return (y * self.weight.float()).to(x.dtype)

@@ -126,8 +126,27 @@ def _qkv_rope_bwd(ctx, dq, dk, dv):
 qkv_rope_op.register_autograd(_qkv_rope_bwd, setup_context=_qkv_rope_setup)
 
 
+class QKVRopeFn(torch.autograd.Function):
+    """The same kernels as t2t::qkv_rope for eager execution (a plain
+    autograd.Function has a fraction of the host cost of the custom op's
+    registered autograd; compiled graphs trace the custom op)."""
+
+    @staticmethod
+    def forward(ctx, qkv, cos, sin, num_heads, pos0):
+        ctx.save_for_backward(cos, sin)
+        ctx.pos0 = pos0
+        return _qkv_rope_impl(qkv, cos, sin, num_heads, pos0)
+
+    @staticmethod
+    def backward(ctx, dq, dk, dv):
+        cos, sin = ctx.saved_tensors
+        return _qkv_rope_bwd_impl(dq, dk, dv, cos, sin, ctx.pos0), None, None, None, None
+
+
 def qkv_rope(qkv: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, num_heads: int,
              pos0: int = 0):
     """Split qkv [B, T, 3 C] into rotated q, k and v, each [B, H, T, D]
     (contiguous), with positions pos0 .. pos0 + T - 1 (table rows)."""
-    return qkv_rope_op(qkv, cos, sin, int(num_heads), int(pos0))
+    if torch.compiler.is_compiling():
+        return qkv_rope_op(qkv, cos, sin, int(num_heads), int(pos0))
+    return QKVRopeFn.apply(qkv, cos, sin, int(num_heads), int(pos0))
