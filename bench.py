@@ -188,6 +188,65 @@ def prologue_stats(dev, T: int, C: int, H: int, reps: int):
     return out
 
 
+def schedule_bench(args, dev):
+    """Density-aware ordering of packs across data-parallel ranks
+    (tagseq2tagseq_amd.schedule).
+      * cost model: 16 packs of the configs[2] generator (T 16384), attention
+        fwd+bwd (H 16, D 128) timed per pack; R^2 of a linear fit of the step
+        time on the exact pair count (pack_pairs, host);
+      * straggler share (idle time of lockstep ranks waiting for the slowest,
+        sum over steps of max - mean over sum of max) of 8 ranks x 64 steps,
+        each rank drawing its own packs, with and without the ordering
+        (window 16), costs = measured-model times of the packs."""
+    from tagseq2tagseq_amd.schedule import DensityOrderedBatches, pack_pairs, straggler_fraction
+    T, H, D = 16384, 16, 128
+    g = torch.Generator().manual_seed(args.seed)
+    q, k, v, do = (torch.randn(1, H, T, D, generator=g).to(torch.bfloat16).to(dev)
+                   for _ in range(4))
+    scale = 1.0 / math.sqrt(D)
+    pairs, ms = [], []
+    for s in range(16):
+        row = synth.linked_lognormal_docs(T, 350.0, 1.0, 2048, 0.15, seed=100 + s)
+        rows_np = [per_token_arrays(row)]
+        doc = torch.from_numpy(rows_np[0][0]).to(dev)[None]
+        qb = torch.from_numpy(rows_np[0][1].view(np.int64)).to(dev)[None]
+        kb = torch.from_numpy(rows_np[0][2].view(np.int64)).to(dev)[None]
+        bm = build_block_mask(doc, qb, kb)
+
+        def step():
+            out, lse2 = attn_fwd(q, k, v, bm, scale)
+            attn_bwd(q, k, v, out, do, lse2, bm, scale)
+
+        ms.append(time_launches(step, max(3, args.reps // 4)))
+        pairs.append(pack_pairs(T, row.spans, row.link_rows))
+    x, y = np.array(pairs, dtype=np.float64), np.array(ms)
+    A = np.stack([x, np.ones_like(x)], 1)
+    coef, *_ = np.linalg.lstsq(A, y, rcond=None)
+    r2 = 1.0 - ((y - A @ coef) ** 2).sum() / ((y - y.mean()) ** 2).sum()
+    # 8 ranks x 64 steps of independent packs, costs from the fitted model
+    ranks, steps, window = 8, 64, 16
+    raw, ordered = [], []
+    for r in range(ranks):
+        packs = [{"ms": float(coef[0] * pack_pairs(T, row.spans, row.link_rows) + coef[1])}
+                 for row in (synth.linked_lognormal_docs(T, 350.0, 1.0, 2048, 0.15,
+                                                         seed=10000 * (r + 1) + k)
+                             for k in range(steps))]
+        raw.append([p["ms"] for p in packs])
+        ordered.append([p["ms"] for p in DensityOrderedBatches(packs, lambda b: b["ms"], window)])
+    f_raw, f_ord = straggler_fraction(np.array(raw)), straggler_fraction(np.array(ordered))
+    print(json.dumps({
+        "metric": "lockstep straggler share at 8 ranks (attention fwd+bwd time model)",
+        "value": round(f_ord, 4), "unit": "fraction of step time idle",
+        "higher_is_better": False, "n_gpus": 1, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": "configs[2] packs, T 16384, H 16, D 128", "ranks": ranks,
+                   "steps": steps, "window": window},
+        "unordered": round(f_raw, 4),
+        "cost_model": {"packs_timed": len(ms), "ms_per_mpair": round(coef[0] * 1e6, 5),
+                       "ms_fixed": round(coef[1], 4), "r2": round(float(r2), 4),
+                       "ms_range": [round(float(y.min()), 4), round(float(y.max()), 4)]},
+    }))
+
+
 def decode_bench(args, dev):
     """Generation on the configs[4] model (12 layers, d768, H12, D64, vocab
     50257, random init) over a T = 16384 - 64 token context packed with the
@@ -384,6 +443,9 @@ def main():
     ap.add_argument("--cpu-threads", type=int, default=min(16, os.cpu_count() or 1))
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device copy (HBM-counter calibration)")
+    ap.add_argument("--schedule", action="store_true",
+                    help="density-aware ordering across ranks: cost-model check on the GPU "
+                         "and the simulated straggler share at 8 ranks")
     ap.add_argument("--decode", action="store_true",
                     help="generation with the key/value cache on the configs[4] model "
                          "(per-token latency, cached vs full recompute, decode kernel roofline)")
@@ -400,6 +462,9 @@ def main():
 
     if args.decode:
         decode_bench(args, dev)
+        return
+    if args.schedule:
+        schedule_bench(args, dev)
         return
     if args.config == 5:
         backbone_step(args, dev)
