@@ -1,6 +1,6 @@
 """Text summaries of rocprofv3 runs of bench.py (kernel durations, HBM traffic).
 
-    python -m tagseq2tagseq_amd.rocprof_summary trace  <kt_dir> <bench_json> <config> > kernel_trace.txt
+    python -m tagseq2tagseq_amd.rocprof_summary trace  <kt_dir> <bench_json> <config> [bench args] > kernel_trace.txt
     python -m tagseq2tagseq_amd.rocprof_summary traffic <fetch_dir> <write_dir> \
         <copy_fetch_dir> <copy_write_dir> <config> > hbm_traffic.txt
 
@@ -24,10 +24,17 @@ from collections import defaultdict
 from typing import Dict, List
 
 WORKLOADS = {
-    2: "doc_causal B2 H12 T8192 D64 bf16",
-    3: "cross_doc_link B1 H16 T16384 D128 bf16",
-    4: "cross_doc_link GQA B1 Hq16 Hkv4 T32768 D128 bf16",
+    "2": "doc_causal B2 H12 T8192 D64 bf16",
+    "3": "cross_doc_link B1 H16 T16384 D128 bf16",
+    "4": "cross_doc_link GQA B1 Hq16 Hkv4 T32768 D128 bf16",
+    "5": "12-layer d768 H12 D64 backbone training step, cross_doc_link T16384 bf16",
+    "decode": "generation on the config-5 model, T~16k context, one token per step",
 }
+DEFAULT_ARGS = "--config {cfg} --no-cpu-baseline --steps 10 --warmup 3"
+
+
+def _label(cfg) -> str:
+    return f"config {cfg}" if str(cfg).isdigit() else str(cfg)
 
 
 def _short(name: str) -> str:
@@ -76,17 +83,20 @@ def copy_counter(path: str, counter: str) -> float:
     return max(vals.values())
 
 
-def trace(kt_dir: str, bench_json: str, cfg: int) -> str:
+def trace(kt_dir: str, bench_json: str, cfg: str, bench_args: str = "") -> str:
     durs = kernel_durations(kt_dir)
+    dbs = glob.glob(f"{kt_dir}/**/*_results.db", recursive=True)
+    out_name = dbs[0].rsplit("/", 1)[-1][:-len("_results.db")] if dbs else "kt"
+    bench_args = bench_args or DEFAULT_ARGS.format(cfg=cfg)
     with open(bench_json) as f:
         bench = json.loads(f.read().strip().splitlines()[-1])
     ev = bench.get("kernels_ms", {})
     lines = [
-        f"# rocprofv3 kernel trace -- config {cfg} ({WORKLOADS.get(cfg, '?')}), MI355X",
+        f"# rocprofv3 kernel trace -- {_label(cfg)} ({WORKLOADS.get(str(cfg), '?')}), MI355X",
         "#",
         "# command (repo root, GPU box):",
-        f"#   rocprofv3 --kernel-trace --stats -d {kt_dir} -o kt -- \\",
-        f"#       python -u bench.py --config {cfg} --no-cpu-baseline --steps 10 --warmup 3",
+        f"#   rocprofv3 --kernel-trace --stats -d {kt_dir} -o {out_name} -- \\",
+        f"#       python -u bench.py {bench_args}",
         "# durations in microseconds over every dispatch of the run (warm-up, timed steps and",
         "# bench.py's per-kernel timing loops); the last column is bench.py's own HIP-event",
         "# mean per call from the JSON line of the same profiled run (token_inputs: the whole",
@@ -102,21 +112,26 @@ def trace(kt_dir: str, bench_json: str, cfg: int) -> str:
     lines.append("")
     lines.append(f"# bench.py line of that run: value {bench.get('value')} {bench.get('unit')}, "
                  f"ms_per_step {bench.get('ms_per_step')}")
+    for key in ("prologue", "decode_kernel"):
+        if key in bench:
+            lines.append(f"# bench.py {key}: {json.dumps(bench[key])}")
     return "\n".join(lines) + "\n"
 
 
-def traffic(fetch_dir: str, write_dir: str, cfetch_dir: str, cwrite_dir: str, cfg: int) -> str:
+def traffic(fetch_dir: str, write_dir: str, cfetch_dir: str, cwrite_dir: str, cfg: str,
+            bench_args: str = "") -> str:
+    bench_args = bench_args or f"--config {cfg} --no-cpu-baseline --steps 2 --warmup 1 --reps 2"
     copy_kib = 1024.0 * 1024.0  # bench.py --copy-calibration copies 1 GiB
     ff = copy_kib / copy_counter(cfetch_dir, "FETCH_SIZE")
     wf = copy_kib / copy_counter(cwrite_dir, "WRITE_SIZE")
     fetch = counter_means(fetch_dir, "FETCH_SIZE")
     write = counter_means(write_dir, "WRITE_SIZE")
     lines = [
-        f"# HBM traffic per launch -- config {cfg} ({WORKLOADS.get(cfg, '?')}), MI355X",
+        f"# HBM traffic per launch -- {_label(cfg)} ({WORKLOADS.get(str(cfg), '?')}), MI355X",
         "#",
         "# commands (repo root, GPU box), one counter per pass:",
-        f"#   rocprofv3 --pmc FETCH_SIZE -d {fetch_dir} -o f -- python -u bench.py --config {cfg} --no-cpu-baseline --steps 2 --warmup 1 --reps 2",
-        f"#   rocprofv3 --pmc WRITE_SIZE -d {write_dir} -o w -- python -u bench.py --config {cfg} --no-cpu-baseline --steps 2 --warmup 1 --reps 2",
+        f"#   rocprofv3 --pmc FETCH_SIZE -d {fetch_dir} -o f -- python -u bench.py {bench_args}",
+        f"#   rocprofv3 --pmc WRITE_SIZE -d {write_dir} -o w -- python -u bench.py {bench_args}",
         "# calibration: the same counters on bench.py --copy-calibration (1 GiB device copies):",
         f"#   rocprofv3 --pmc FETCH_SIZE -d {cfetch_dir} -o cf -- python -u bench.py --copy-calibration",
         f"#   rocprofv3 --pmc WRITE_SIZE -d {cwrite_dir} -o cw -- python -u bench.py --copy-calibration",
@@ -135,9 +150,9 @@ def traffic(fetch_dir: str, write_dir: str, cfetch_dir: str, cwrite_dir: str, cf
 
 def main(argv: List[str]) -> None:
     if len(argv) >= 4 and argv[0] == "trace":
-        sys.stdout.write(trace(argv[1], argv[2], int(argv[3])))
+        sys.stdout.write(trace(argv[1], argv[2], argv[3], " ".join(argv[4:])))
     elif len(argv) >= 6 and argv[0] == "traffic":
-        sys.stdout.write(traffic(argv[1], argv[2], argv[3], argv[4], int(argv[5])))
+        sys.stdout.write(traffic(argv[1], argv[2], argv[3], argv[4], argv[5], " ".join(argv[6:])))
     else:
         raise SystemExit(__doc__)
 
