@@ -320,22 +320,24 @@ __global__ __launch_bounds__(kDkdvThreads, 1) void bwd_dkdv_kernel(BwdParams p) 
   }
 }
 
-template <int D>
-struct DqSmem {
-  __bf16 k[kTile * pitch<D>()];  // padded rows
-  __bf16 v[kTile * pitch<D>()];
-};
-
 // dQ for one (b, query head, 128-query tile).  Per wave 32 queries; S^T and
 // dP^T put the query in the lane, dS^T feeds dQ^T += K^T dS^T as B operand.
+// The row's KV tiles stream through LDS as 64-key halves (one unit each for
+// K and V rows), refilled by direct global->LDS copies issued right after the
+// barrier that retired them, so each copy has one half of compute to land in;
+// the tile bitmaps travel one tile ahead the same way.
 template <int D>
 __global__ __launch_bounds__(kThreads, 2) void bwd_dq_kernel(BwdParams p) {
   constexpr int KS = D / 16;
   constexpr int DT = D / 32;
-  __shared__ DqSmem<D> sm;
+  using U = UnitDma<D>;
+  constexpr int kUnit = U::kRows * pitch<D>();
+  __shared__ __bf16 k_lo[kUnit], k_hi[kUnit], v_lo[kUnit], v_hi[kUnit];
+  __shared__ uint32_t bits_lds[2][kTile * 4];
+  __shared__ uint4 dma_scratch[64];  // sink of the copies no wave owns
 
   const int h = blockIdx.x, b = blockIdx.z;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x, wave = uniform(tid >> 6), lane = tid & 63;
   const int g = lane >> 5, n = lane & 31;
   const int hk = h / (p.Hq / p.Hkv);
   const int mb = p.m.Bm > 1 ? b : 0;
@@ -367,70 +369,128 @@ __global__ __launch_bounds__(kThreads, 2) void bwd_dq_kernel(BwdParams p) {
     delta = p.delta[((size_t)b * p.Hq + h) * T + qrow];
   }
 
-  const auto krs = slice_rsrc(p.k + b * p.k_sb + hk * p.k_sh, p.k_st, T, D);
-  const auto vrs = slice_rsrc(p.v + b * p.v_sb + hk * p.v_sh, p.v_st, T, D);
+  const __bf16* kbase = p.k + b * p.k_sb + hk * p.k_sh;
+  const __bf16* vbase = p.v + b * p.v_sb + hk * p.v_sh;
+  int koff[U::kPerWave + 1], voff[U::kPerWave + 1];
+#pragma unroll
+  for (int j = 0; j < U::kPerWave; ++j) {
+    koff[j] = unit_dma_offset<D>(wave + kWaves * j, p.k_st, lane);
+    voff[j] = unit_dma_offset<D>(wave + kWaves * j, p.v_st, lane);
+  }
+  koff[U::kPerWave] = unit_dma_offset<D>(U::kInsts - 1, p.k_st, lane);
+  voff[U::kPerWave] = unit_dma_offset<D>(U::kInsts - 1, p.v_st, lane);
+
   const size_t row = (size_t)mb * nt + qt;
   const int npart = uniform(p.m.kv_num[row]);
   const int nfull = uniform(p.m.full_kv_num[row]);
+  const int ntiles = npart + nfull;
   const int32_t* pidx = p.m.kv_idx + row * nt;
   const int32_t* fidx = p.m.full_kv_idx + row * nt;
-  const uint32_t* bits_base = p.m.tile_bits + (size_t)p.m.kv_bits_off[row] * kTileBitsWords + qloc * 4;
+  const uint32_t* bits_row = p.m.tile_bits + (size_t)p.m.kv_bits_off[row] * kTileBitsWords;
+
+  // KV tile indices of the row, 64 iterations per chunk (lane j: iteration
+  // 64 * chunk + j), read back with readlane.
+  auto load_chunk = [&](int chunk) {
+    const int it = 64 * chunk + lane;
+    return it < npart ? pidx[it] : (it < ntiles ? fidx[it - npart] : 0);
+  };
+  int tiles_v = load_chunk(0);
+  auto tile_of = [&](int it) { return __builtin_amdgcn_readlane(tiles_v, it & 63); };
+  const auto krs = slice_rsrc(kbase, p.k_st, T, D);
+  const auto vrs = slice_rsrc(vbase, p.v_st, T, D);
+  const int k_row2 = (int)p.k_st * 2, v_row2 = (int)p.v_st * 2;
+  // K and V rows [t0, t0 + 64) into one half's units (rows past T read zero).
+  auto load_half = [&](__bf16* kd, __bf16* vd, int t0) {
+    unit_dma<D>(kd, krs, koff, t0 * k_row2, wave, 0, dma_scratch);
+    unit_dma<D>(vd, vrs, voff, t0 * v_row2, wave, 1, dma_scratch);
+  };
+  // Row-major half (128 queries x 4 words) of tile it's bitmap slot; waves w
+  // and w + 2 copy the same KiB.  Tiles without a bitmap copy zeros.
+  auto load_bits = [&](int it) {
+    const bool has = it < npart;
+    const auto rs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint32_t*>(bits_row + (has ? (size_t)it * kTileBitsWords : 0)), 0,
+        has ? kTile * 16 : 0, 0x00020000);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        rs, (__attribute__((address_space(3))) void*)(&bits_lds[it & 1][(wave & 1) * 256]), 16,
+        (wave & 1) * 1024 + lane * 16, 0, 0, 0);
+  };
 
   f32x16 dqacc[DT];
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) dqacc[dt] = f32x16{};
 
-  for (int it = 0; it < npart + nfull; ++it) {
-    const bool partial = it < npart;
-    const int kt = uniform(partial ? pidx[it] : fidx[it - npart]);
-    const int k0 = kt * kTile;
-    uint4 mbits = make_uint4(~0u, ~0u, ~0u, ~0u);
-    if (partial) mbits = *reinterpret_cast<const uint4*>(bits_base + (size_t)it * kTileBitsWords);
-    __syncthreads();
-    load_tile_lds<D>(sm.k, krs, p.k_st, k0, tid);
-    load_tile_lds<D>(sm.v, vrs, p.v_st, k0, tid);
-    __syncthreads();
-    const uint32_t w4[4] = {mbits.x, mbits.y, mbits.z, mbits.w};
-
+  // One 32-key block: rows 32 j .. 32 j + 31 of a half's units; w = the
+  // lane's bitmap word (all ones for full tiles).
+  auto block = [&](const __bf16* ku, const __bf16* vu, uint32_t w, int j) {
+    if (__ballot(w != 0u) == 0ull) return;
+    const bool mixed = __ballot(w != ~0u) != 0ull;
+    f32x16 sacc = mixed ? mask_bias(~(w >> g)) : f32x16{};
+    f32x16 dpacc = f32x16{};
+    __builtin_amdgcn_s_setprio(1);  // MFMA runs at raised wave priority
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      if (__ballot(w4[j] != 0u) == 0ull) continue;
-      const bool mixed = __ballot(w4[j] != ~0u) != 0ull;
-      f32x16 sacc, dpacc;
-      __builtin_amdgcn_s_setprio(1);  // MFMA runs at raised wave priority
-      {
-        const bf16x8 ka = lds_row8<D>(sm.k, 32 * j + tok_perm(n), 8 * g);
-        const bf16x8 va = lds_row8<D>(sm.v, 32 * j + tok_perm(n), 8 * g);
-        if (mixed) sacc = mfma32(ka, qf[0], mask_bias(~(w4[j] >> g)));
-        else sacc = mfma32(ka, qf[0], f32x16{});
-        dpacc = mfma32(va, dof[0], f32x16{});
-      }
-#pragma unroll
-      for (int s = 1; s < KS; ++s) {
-        const bf16x8 ka = lds_row8<D>(sm.k, 32 * j + tok_perm(n), 16 * s + 8 * g);
-        const bf16x8 va = lds_row8<D>(sm.v, 32 * j + tok_perm(n), 16 * s + 8 * g);
-        sacc = mfma32(ka, qf[s], sacc);
-        dpacc = mfma32(va, dof[s], dpacc);
-      }
-      __builtin_amdgcn_s_setprio(0);
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const float pv = fast_exp2(fmaf(sacc[i], c, neg_lse));
-        dpacc[i] = pv * (dpacc[i] - delta);  // dS^T
-      }
-      // dQ^T += K^T dS^T (contraction over the 32 keys of block j).
-      __builtin_amdgcn_s_setprio(1);
-#pragma unroll
-      for (int h2 = 0; h2 < 2; ++h2) {
-        const bf16x8 sb = pack_half(dpacc, h2);
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) {
-          const bf16x8 ka = lds_col8<D>(sm.k, 32 * j + 16 * h2, 32 * dt, lane);
-          dqacc[dt] = mfma32(ka, sb, dqacc[dt]);
-        }
-      }
-      __builtin_amdgcn_s_setprio(0);
+    for (int s = 0; s < KS; ++s) {
+      const bf16x8 ka = lds_row8<D>(ku, 32 * j + tok_perm(n), 16 * s + 8 * g);
+      const bf16x8 va = lds_row8<D>(vu, 32 * j + tok_perm(n), 16 * s + 8 * g);
+      sacc = mfma32(ka, qf[s], sacc);
+      dpacc = mfma32(va, dof[s], dpacc);
     }
+    // LDS reads four MFMAs ahead of their use.
+    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+    for (int i = 0; i < 2 * KS - 4; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+    __builtin_amdgcn_s_setprio(0);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const float pv = fast_exp2(fmaf(sacc[i], c, neg_lse));
+      dpacc[i] = pv * (dpacc[i] - delta);  // dS^T
+    }
+    // dQ^T += K^T dS^T (contraction over the 32 keys of the block).
+    __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+    for (int h2 = 0; h2 < 2; ++h2) {
+      const bf16x8 sb = pack_half(dpacc, h2);
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        const bf16x8 ka = lds_col8<D>(ku, 32 * j + 16 * h2, 32 * dt, lane);
+        dqacc[dt] = mfma32(ka, sb, dqacc[dt]);
+      }
+    }
+    __builtin_amdgcn_s_setprio(0);
+  };
+
+  int k0_next = ntiles > 0 ? tile_of(0) * kTile : 0;
+  if (ntiles > 0) {
+    load_half(k_lo, v_lo, k0_next);
+    if (npart > 0) load_bits(0);
+  }
+  for (int it = 0; it < ntiles; ++it) {
+    const bool partial = it < npart;
+    const int k0 = k0_next;
+    // Keys [k0, k0 + 64): its units and bitmap have landed; the other half's
+    // units are free again.
+    dma_barrier();
+    uint4 mbits = make_uint4(~0u, ~0u, ~0u, ~0u);
+    if (partial) mbits = *reinterpret_cast<const uint4*>(&bits_lds[it & 1][qloc * 4]);
+    load_half(k_hi, v_hi, k0 + 64);
+    block(k_lo, v_lo, mbits.x, 0);
+    block(k_lo, v_lo, mbits.y, 1);
+
+    // Keys [k0 + 64, k0 + 128); the first half's units are free again.
+    dma_barrier();
+    const bool more = it + 1 < ntiles;
+    if (more) {
+      if (((it + 1) & 63) == 0) tiles_v = load_chunk((it + 1) >> 6);
+      k0_next = tile_of(it + 1) * kTile;
+      load_half(k_lo, v_lo, k0_next);
+      load_bits(it + 1);
+    }
+    block(k_hi, v_hi, mbits.z, 0);
+    block(k_hi, v_hi, mbits.w, 1);
   }
 
   if (qvalid) {
