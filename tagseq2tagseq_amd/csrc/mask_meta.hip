@@ -21,13 +21,24 @@
 // rectangle.  Packed documents give 1-3 runs per 128 tokens, so a tile costs a
 // handful of evaluations instead of 16384.
 //
-// Launches: (1) classify every tile, (2) row and column lists, (3) bitmap
-// slot offsets and launch orders, (4) partial-tile bitmaps.
+// Launches: (1) classify every tile, (2) row and column lists, (3) partial-
+// tile bitmaps; the third also writes the bitmap slot offsets (each row's
+// column-0 work-group) and the launch orders (work-group (0, 0) of each mask
+// row), so no launch waits on a single work-group.
 #include "attn_kernels.h"
 
 namespace t2t {
 
 namespace {
+
+// Lower-triangle tile of linear index L (row-major over qt, kt <= qt).
+__device__ __forceinline__ void tri_tile(int L, int& qt, int& kt) {
+  int r = (int)((sqrtf(8.f * (float)L + 1.f) - 1.f) * 0.5f);
+  while ((r + 1) * (r + 2) / 2 <= L) ++r;  // exact despite float rounding
+  while (r * (r + 1) / 2 > L) --r;
+  qt = r;
+  kt = L - r * (r + 1) / 2;
+}
 
 struct TokSig {
   int32_t doc;
@@ -127,20 +138,21 @@ __device__ void wave_ordered(const int8_t* cls, int stride, int n, int8_t want,
 
 }  // namespace
 
-// (1) grid (nt, nt, Bm); block 64: one wave decides one tile (kt = x, qt = y).
+// (1) grid (nt (nt + 1) / 2, Bm); block 64: one wave decides one tile of the
+// lower triangle (kt <= qt) and writes its mirror above the diagonal as skip
+// (every pair there has kv > q).
 __global__ __launch_bounds__(64) void mask_classify_tiles(
     const int32_t* __restrict__ doc_all, const uint64_t* __restrict__ qbits_all,
     const uint64_t* __restrict__ kvbits_all, int T, int words, MaskOut out) {
   __shared__ int q_starts[kTile + 1];
   __shared__ int kv_starts[kTile + 1];
   const int nt = out.nt;
-  const int kt = blockIdx.x, qt = blockIdx.y, b = blockIdx.z;
+  const int b = blockIdx.y;
+  int qt, kt;
+  tri_tile(blockIdx.x, qt, kt);
   const int lane = threadIdx.x;
   int8_t* dst = out.tile_class + ((size_t)b * nt + qt) * nt + kt;
-  if (kt > qt) {  // every pair has kv > q
-    if (lane == 0) *dst = kSkip;
-    return;
-  }
+  if (lane == 0 && kt < qt) out.tile_class[((size_t)b * nt + kt) * nt + qt] = kSkip;
   const int32_t* doc = doc_all + (size_t)b * T;
   const uint64_t* qbits = qbits_all + (size_t)b * words * T;
   const uint64_t* kvbits = kvbits_all + (size_t)b * words * T;
@@ -191,48 +203,58 @@ __global__ __launch_bounds__(kThreads) void mask_lists(MaskOut out) {
     wave_ordered(grid + i, nt, nt, kFull, out.full_q_num + r, out.full_q_idx + r * nt);
 }
 
-// (3) grid (1); block 256.  kv_bits_off = exclusive prefix sum of kv_num over
-// (b, row); row / column launch orders ranked by descending non-skip tile
-// count (ties: higher index first).
-__global__ __launch_bounds__(kThreads) void mask_offsets_schedule(MaskOut out) {
-  __shared__ int scan[kThreads];
-  const int nt = out.nt;
-  const int tid = threadIdx.x;
-  const int n = out.Bm * nt;
-  int carry = 0;
-  for (int c = 0; c < n; c += kThreads) {
-    const int i = c + tid;
-    const int v = i < n ? out.kv_num[i] : 0;
-    scan[tid] = v;
-    __syncthreads();
-    for (int off = 1; off < kThreads; off <<= 1) {
-      const int add = tid >= off ? scan[tid - off] : 0;
+namespace {
+
+constexpr int kRankChunk = 512;
+
+// Launch orders of mask row b, by the whole work-group: rows / columns ranked
+// by descending non-skip tile count (ties: higher index first), the counts
+// staged through LDS in chunks.
+__device__ void rank_orders(const MaskOut& out, int b, int* rtot, int* ctot) {
+  const int nt = out.nt, tid = threadIdx.x;
+  const int32_t* rn = out.kv_num + (size_t)b * nt;
+  const int32_t* rf = out.full_kv_num + (size_t)b * nt;
+  const int32_t* cn = out.q_num + (size_t)b * nt;
+  const int32_t* cf = out.full_q_num + (size_t)b * nt;
+  for (int i0 = 0; i0 < nt; i0 += kThreads) {
+    const int i = i0 + tid;
+    const int ri = i < nt ? rn[i] + rf[i] : 0, ci = i < nt ? cn[i] + cf[i] : 0;
+    int rr = 0, rc = 0;
+    for (int j0 = 0; j0 < nt; j0 += kRankChunk) {
+      const int m = min(kRankChunk, nt - j0);
       __syncthreads();
-      scan[tid] += add;
-      __syncthreads();
-    }
-    if (i < n) out.kv_bits_off[i] = carry + scan[tid] - v;
-    carry += scan[kThreads - 1];
-    __syncthreads();
-  }
-  for (int b = 0; b < out.Bm; ++b) {
-    const int32_t* rn = out.kv_num + (size_t)b * nt;
-    const int32_t* rf = out.full_kv_num + (size_t)b * nt;
-    const int32_t* cn = out.q_num + (size_t)b * nt;
-    const int32_t* cf = out.full_q_num + (size_t)b * nt;
-    for (int i = tid; i < nt; i += kThreads) {
-      const int ri = rn[i] + rf[i], ci = cn[i] + cf[i];
-      int rr = 0, rc = 0;
-      for (int j = 0; j < nt; ++j) {
-        const int rj = rn[j] + rf[j], cj = cn[j] + cf[j];
-        rr += (rj > ri) || (rj == ri && j > i);
-        rc += (cj > ci) || (cj == ci && j > i);
+      for (int j = tid; j < m; j += kThreads) {
+        rtot[j] = rn[j0 + j] + rf[j0 + j];
+        ctot[j] = cn[j0 + j] + cf[j0 + j];
       }
+      __syncthreads();
+      for (int j = 0; j < m; ++j) {
+        const int rj = rtot[j], cj = ctot[j];
+        rr += (rj > ri) || (rj == ri && j0 + j > i);
+        rc += (cj > ci) || (cj == ci && j0 + j > i);
+      }
+    }
+    if (i < nt) {
       out.row_order[(size_t)b * nt + rr] = i;
       out.col_order[(size_t)b * nt + rc] = i;
     }
   }
 }
+
+// Exclusive prefix of kv_num over (mask row, row) up to entry e = b * nt + qt,
+// by one wave: the first bitmap slot of that row's partial tiles.
+__device__ int row_slot_offset(const MaskOut& out, int e, int lane) {
+  int sum = 0;
+  for (int c = 0; c < e; c += 64) {
+    const int j = c + lane;
+    sum += j < e ? out.kv_num[j] : 0;
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
+  return sum;
+}
+
+}  // namespace
 
 namespace {
 
@@ -259,7 +281,8 @@ __device__ __forceinline__ bool lds_pair_allowed(int32_t da, int32_t db, const u
 
 }  // namespace
 
-// (4) grid (nt, nt, Bm); block 256.  For a partial tile (kt = x, qt = y): its
+// (3) grid (nt (nt + 1) / 2, Bm); block 256.  For a partial tile of the lower
+// triangle: its
 // slot (row-major numbering over (b, qt, list position)), both bitmap
 // orientations, and its entry in the column's slot list.  A row of the
 // bitmap is built run by run: within a run of keys with one signature the
@@ -271,13 +294,22 @@ __global__ __launch_bounds__(kThreads) void mask_tile_bits(
   __shared__ int32_t qdoc[kTile], kdoc[kTile];
   __shared__ uint64_t qb[kMaxWords][kTile], kb[kMaxWords][kTile];
   __shared__ int q_starts[kTile + 1], kv_starts[kTile + 1];
-  __shared__ int n_qr, n_kr, pos_row, pos_col;
+  __shared__ int n_qr, n_kr, pos_row, pos_col, row_off;
+  __shared__ int rtot[kRankChunk], ctot[kRankChunk];
   const int nt = out.nt;
-  const int kt = blockIdx.x, qt = blockIdx.y, b = blockIdx.z;
-  if (kt > qt) return;
+  const int b = blockIdx.y;
+  int qt, kt;
+  tri_tile(blockIdx.x, qt, kt);
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  // Work-group (0, 0) of a mask row also writes its launch orders, and
+  // work-group (0, qt) the row's first bitmap slot (kv_bits_off).
+  if (kt == 0 && qt == 0) rank_orders(out, b, rtot, ctot);
+  if (kt == 0 && wave == 0) {
+    const int off = row_slot_offset(out, b * nt + qt, lane);
+    if (lane == 0) out.kv_bits_off[(size_t)b * nt + qt] = off;
+  }
   const int8_t* grid = out.tile_class + (size_t)b * nt * nt;
   if (grid[(size_t)qt * nt + kt] != kPartial) return;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int32_t* doc = doc_all + (size_t)b * T;
   const uint64_t* qbits = qbits_all + (size_t)b * words * T;
   const uint64_t* kvbits = kvbits_all + (size_t)b * words * T;
@@ -289,7 +321,11 @@ __global__ __launch_bounds__(kThreads) void mask_tile_bits(
       const int j = c + lane;
       cnt += __popcll(__ballot(j < kt && grid[(size_t)qt * nt + j] == kPartial));
     }
-    if (lane == 0) pos_row = cnt;
+    const int off = row_slot_offset(out, b * nt + qt, lane);
+    if (lane == 0) {
+      pos_row = cnt;
+      row_off = off;
+    }
   } else if (wave == 1) {  // position among the column's partial tiles (rows < qt)
     int cnt = 0;
     for (int c = 0; c < qt; c += 64) {
@@ -314,7 +350,7 @@ __global__ __launch_bounds__(kThreads) void mask_tile_bits(
     for (int w = 0; w < words; ++w) kb[w][c] = t < T ? kvbits[(size_t)w * T + t] : 0ull;
   }
   __syncthreads();
-  const int slot = out.kv_bits_off[(size_t)b * nt + qt] + pos_row;
+  const int slot = row_off + pos_row;
   uint32_t acc[4] = {0u, 0u, 0u, 0u};
   if (tid < kTile) {
     // row orientation: query q0 + tid against the tile's keys
@@ -359,15 +395,12 @@ hipError_t launch_mask_meta(const int32_t* doc, const uint64_t* qbits, const uin
                             int T, int words, const MaskOut& out, hipStream_t stream) {
   const int nt = out.nt;
   if (nt == 0 || out.Bm == 0) return hipSuccess;
-  const dim3 tiles(nt, nt, out.Bm);
+  const dim3 tiles((unsigned)(nt * (nt + 1) / 2), out.Bm);
   hipLaunchKernelGGL(mask_classify_tiles, tiles, dim3(64), 0, stream, doc, qbits, kvbits, T,
                      words, out);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(mask_lists, dim3(nt, out.Bm), dim3(kThreads), 0, stream, out);
-  e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(mask_offsets_schedule, dim3(1), dim3(kThreads), 0, stream, out);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(mask_tile_bits, tiles, dim3(kThreads), 0, stream, doc, qbits, kvbits, T,
