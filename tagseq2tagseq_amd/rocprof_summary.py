@@ -3,6 +3,12 @@
     python -m tagseq2tagseq_amd.rocprof_summary trace  <kt_dir> <bench_json> <config> [bench args] > kernel_trace.txt
     python -m tagseq2tagseq_amd.rocprof_summary traffic <fetch_dir> <write_dir> \
         <copy_fetch_dir> <copy_write_dir> <config> > hbm_traffic.txt
+    python -m tagseq2tagseq_amd.rocprof_summary insts <sq_dir> <config> [bench args] > insts.txt
+
+`insts` reads one `--pmc` pass of SQ instruction counters (SQ_INSTS_VALU,
+SQ_INSTS_MFMA, SQ_INSTS_LDS, SQ_INSTS_SALU, SQ_INSTS_VALU_TRANS_F32,
+SQ_INSTS_VMEM, SQ_VALU_MFMA_BUSY_CYCLES, SQ_BUSY_CYCLES) and lists, per
+kernel, the instructions issued per MFMA.
 
 `trace` reads a `rocprofv3 --kernel-trace` database and lists, per kernel,
 the number of dispatches and their mean / median / min / max duration next to
@@ -148,9 +154,46 @@ def traffic(fetch_dir: str, write_dir: str, cfetch_dir: str, cwrite_dir: str, cf
     return "\n".join(lines) + "\n"
 
 
+INST_COUNTERS = ["SQ_INSTS_VALU", "SQ_INSTS_MFMA", "SQ_INSTS_LDS", "SQ_INSTS_SALU",
+                 "SQ_INSTS_VALU_TRANS_F32", "SQ_INSTS_VMEM", "SQ_VALU_MFMA_BUSY_CYCLES",
+                 "SQ_BUSY_CYCLES"]
+
+
+def insts(sq_dir: str, cfg: str, bench_args: str = "") -> str:
+    bench_args = bench_args or f"--config {cfg} --no-cpu-baseline --steps 2 --warmup 1 --reps 2"
+    means = {c: counter_means(sq_dir, c) for c in INST_COUNTERS}
+    lines = [
+        f"# SQ instruction counters per dispatch -- {_label(cfg)} ({WORKLOADS.get(str(cfg), '?')}), MI355X",
+        "#",
+        "# command (repo root, GPU box), one pass:",
+        f"#   rocprofv3 --pmc {' '.join(INST_COUNTERS)} -d {sq_dir} -o sq -- \\",
+        f"#       python -u bench.py {bench_args}",
+        "# instructions issued per MFMA: SQ_INSTS_VALU as counted (whether it includes the",
+        "# MFMA instructions themselves is not separated here), transcendental VALU, LDS,",
+        "# SALU and vector-memory instructions; MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES summed",
+        "# over the dispatch.",
+        "",
+        f"{'kernel':28s} {'MFMA':>10s} {'VALU/MFMA':>10s} {'TRANS/MFMA':>11s} {'LDS/MFMA':>9s} "
+        f"{'SALU/MFMA':>10s} {'VMEM/MFMA':>10s} {'MFMA busy':>12s}",
+    ]
+    kernels = sorted(means["SQ_INSTS_MFMA"], key=lambda k: -means["SQ_INSTS_MFMA"][k])
+    for k in kernels:
+        mf = means["SQ_INSTS_MFMA"].get(k, 0.0)
+        if mf <= 0:
+            continue
+        g = lambda c: means[c].get(k, 0.0) / mf
+        lines.append(f"{k:28s} {mf:10.0f} {g('SQ_INSTS_VALU'):10.2f} "
+                     f"{g('SQ_INSTS_VALU_TRANS_F32'):11.2f} {g('SQ_INSTS_LDS'):9.2f} "
+                     f"{g('SQ_INSTS_SALU'):10.2f} {g('SQ_INSTS_VMEM'):10.2f} "
+                     f"{means['SQ_VALU_MFMA_BUSY_CYCLES'].get(k, 0.0):12.0f}")
+    return "\n".join(lines) + "\n"
+
+
 def main(argv: List[str]) -> None:
     if len(argv) >= 4 and argv[0] == "trace":
         sys.stdout.write(trace(argv[1], argv[2], argv[3], " ".join(argv[4:])))
+    elif len(argv) >= 3 and argv[0] == "insts":
+        sys.stdout.write(insts(argv[1], argv[2], " ".join(argv[3:])))
     elif len(argv) >= 6 and argv[0] == "traffic":
         sys.stdout.write(traffic(argv[1], argv[2], argv[3], argv[4], argv[5], " ".join(argv[6:])))
     else:
