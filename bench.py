@@ -556,6 +556,7 @@ def main():
     t_pre = time_launches(ph.preprocess, args.reps)
     t_dkdv = time_launches(ph.dkdv, args.reps)
     t_dq = time_launches(ph.dq_pass, args.reps)
+    t_bwd = time_launches(ph.whole, args.reps)
 
     base = D * n_pairs * Hq
     kernels = {
@@ -621,6 +622,10 @@ def main():
             "bwd_dkdv_kernel": round(t_dkdv, 4),
             "bwd_dq_kernel": round(t_dq, 4),
         },
+        # The step's backward is t2t_attn_bwd: dQ computing Delta itself, then
+        # dK/dV (bwd_delta above is the separate-phase entry point's launch).
+        "attn_bwd_ms": {"t2t_attn_bwd (dQ+Delta, dK/dV)": round(t_bwd, 4),
+                        "dQ+Delta (difference)": round(t_bwd - t_dkdv, 4)},
         "mask_meta": {"us": round(t_meta * 1e3, 2), "bytes": int(meta_bytes),
                       "GBps": round(meta_bytes / (t_meta * 1e-3) / 1e9, 2)},
         "token_inputs": {"us": round(t_tok * 1e3, 2), "bytes": int(tok_bytes),

@@ -156,7 +156,8 @@ int t2t_attn_fwd(const t2t_tensor *q, const t2t_tensor *k, const t2t_tensor *v,
  * Masked attention backward.  Replaces flex_attention_backward as driven by
  * FlexAttentionAutogradOp.backward (torch/_higher_order_ops/flex_attention.py:689-767;
  * eager arithmetic sdpa_dense_backward :825-994).
- * delta: float[B][Hq][T] workspace (overwritten).  dq like q; dk/dv like k/v
+ * delta: float[B][Hq][T] workspace, overwritten with rowsum(O * dO) by the dQ
+ * launch (which runs first and computes it) and read by dK/dV.  dq like q; dk/dv like k/v
  * (summed over each GQA group, written, not accumulated).  No atomics: the
  * result is bitwise deterministic.
  */
@@ -168,8 +169,9 @@ int t2t_attn_bwd(const t2t_tensor *q, const t2t_tensor *k, const t2t_tensor *v,
                  void *stream);
 
 /*
- * The three phases t2t_attn_bwd runs, callable separately (for example to
- * run dK/dV and dQ on two streams once Delta is ready).  Same conventions:
+ * The backward's phases, callable separately (for example to run dK/dV and
+ * dQ on two streams once Delta is ready; t2t_attn_bwd itself runs a dQ that
+ * also writes Delta, then dK/dV).  Same conventions:
  *   preprocess: delta[b][h][t] = sum_d o * dout  (sdpa_dense_backward :910-914)
  *   dkdv:       dk, dv  (KV-tile-major, walks q_num/q_idx + full_q_*)
  *   dq:         dq      (Q-tile-major, walks kv_num/kv_idx + full_kv_*)

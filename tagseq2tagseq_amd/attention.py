@@ -141,7 +141,8 @@ def attn_bwd(q, k, v, out, dout, lse2, block_mask, scale: float):
 class BwdPhases:
     """The three backward launches bound to fixed buffers (t2t_attn_bwd_preprocess,
     t2t_attn_bwd_dkdv, t2t_attn_bwd_dq), for callers that schedule or time
-    them separately."""
+    them separately, and ``whole`` = t2t_attn_bwd on the same buffers (its dQ
+    launch computes Delta itself, then dK/dV)."""
 
     def __init__(self, q, k, v, out, dout, lse2, block_mask: T2TBlockMask, scale: float):
         self.B, self.Hq, self.T, self.D = q.shape
@@ -183,6 +184,15 @@ class BwdPhases:
             self.B, self.Hq, self.Hkv, self.T, self.D, self._dtype, self._scale,
             ctypes.byref(self._mask), _stream_ptr(self.delta))
         _lib.check(rc, "t2t_attn_bwd_dq")
+
+    def whole(self):
+        v = self._v
+        rc = _lib.lib().t2t_attn_bwd(
+            *[ctypes.byref(v[n]) for n in ("q", "k", "v", "o", "do")], self._lse2,
+            self.delta.data_ptr(), *[ctypes.byref(v[n]) for n in ("dq", "dk", "dv")],
+            self.B, self.Hq, self.Hkv, self.T, self.D, self._dtype, self._scale,
+            ctypes.byref(self._mask), _stream_ptr(self.delta))
+        _lib.check(rc, "t2t_attn_bwd")
 
 
 class T2TFlexAttentionFn(torch.autograd.Function):

@@ -8,7 +8,8 @@
 //   dQ = dS K * scale                 dK = dS^T Q * scale
 // with dK / dV summed over the query heads that share a KV head (GQA).
 //
-// Three launches, none of them atomic:
+// Launches, none of them atomic (t2t_attn_bwd runs 3 then 2, with 3
+// computing Delta for its rows; the separate phases run 1, 2, 3):
 //   1. bwd_delta:  Delta per query row.
 //   2. bwd_dkdv:   one work-group per (b, kv head, 128-key tile); walks the
 //                  column's partial and full query tiles (q_num_blocks /
@@ -35,6 +36,7 @@ struct BwdParams {
   float* delta;       // [B][Hq][T]
   int B, Hq, Hkv, T;
   float scale, scale_log2;
+  int fuse_delta;  // dQ computes and writes Delta itself (kBwdDqDelta)
   MaskTables m;
 };
 
@@ -326,6 +328,9 @@ __global__ __launch_bounds__(kDkdvThreads, 1) void bwd_dkdv_kernel(BwdParams p) 
 // K and V rows), refilled by direct global->LDS copies issued right after the
 // barrier that retired them, so each copy has one half of compute to land in;
 // the tile bitmaps travel one tile ahead the same way.
+// With p.fuse_delta the rows' Delta = rowsum(O * dO) is computed here (from
+// the dO rows already held in registers and one read of the O rows) and
+// written for the dK/dV launch that follows, instead of read from bwd_delta.
 template <int D>
 __global__ __launch_bounds__(kThreads, 2) void bwd_dq_kernel(BwdParams p) {
   constexpr int KS = D / 16;
@@ -349,25 +354,49 @@ __global__ __launch_bounds__(kThreads, 2) void bwd_dq_kernel(BwdParams p) {
   const bool qvalid = qrow < T;
   const float c = p.scale_log2;
 
-  bf16x8 qf[KS], dof[KS];
+  // The row's KV tile list first: its first chunk is read back (readlane)
+  // before the first K/V copy, and loads complete in issue order, so that
+  // wait does not also wait for the Q / dO / O rows issued after it.
+  const size_t row = (size_t)mb * nt + qt;
+  const int npart = uniform(p.m.kv_num[row]);
+  const int nfull = uniform(p.m.full_kv_num[row]);
+  const int ntiles = npart + nfull;
+  const int32_t* pidx = p.m.kv_idx + row * nt;
+  const int32_t* fidx = p.m.full_kv_idx + row * nt;
+  const uint32_t* bits_row = p.m.tile_bits + (size_t)p.m.kv_bits_off[row] * kTileBitsWords;
+  // KV tile indices of the row, 64 iterations per chunk (lane j: iteration
+  // 64 * chunk + j), read back with readlane.
+  auto load_chunk = [&](int chunk) {
+    const int it = 64 * chunk + lane;
+    return it < npart ? pidx[it] : (it < ntiles ? fidx[it - npart] : 0);
+  };
+  int tiles_v = load_chunk(0);
+
+  // Rows past T read row 0: a query row only reaches its own dQ column,
+  // which is not stored, and its P is zero (neg_lse = -inf).
+  const int qr = qvalid ? qrow : 0;
+  const size_t rowstat = ((size_t)b * p.Hq + h) * T + qr;
+  bf16x8 qf[KS], dof[KS], of[KS];
   {
-    const int qr = qvalid ? qrow : 0;
     const __bf16* qp = p.q + b * p.q_sb + h * p.q_sh + (int64_t)qr * p.q_st;
     const __bf16* dp = p.dout + b * p.do_sb + h * p.do_sh + (int64_t)qr * p.do_st;
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
-      const bf16x8 a = *reinterpret_cast<const bf16x8*>(qp + 16 * s + 8 * g);
-      const bf16x8 cc = *reinterpret_cast<const bf16x8*>(dp + 16 * s + 8 * g);
-      qf[s] = qvalid ? a : bf16x8{};
-      dof[s] = qvalid ? cc : bf16x8{};
+      qf[s] = *reinterpret_cast<const bf16x8*>(qp + 16 * s + 8 * g);
+      dof[s] = *reinterpret_cast<const bf16x8*>(dp + 16 * s + 8 * g);
     }
   }
-  float neg_lse = -INFINITY, delta = 0.f;
-  if (qvalid) {
-    const float l = p.lse2[((size_t)b * p.Hq + h) * T + qrow];
-    neg_lse = (l == -INFINITY) ? -INFINITY : -l;  // fully masked row: P = 0
-    delta = p.delta[((size_t)b * p.Hq + h) * T + qrow];
+  if (p.fuse_delta) {
+    // Lane (g, n) holds elements 16 s + 8 g .. + 7 of its row's dO; the
+    // matching O elements give half the row's Delta = rowsum(O * dO).
+    const __bf16* op = p.o + b * p.o_sb + h * p.o_sh + (int64_t)qr * p.o_st;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) of[s] = *reinterpret_cast<const bf16x8*>(op + 16 * s + 8 * g);
   }
+  const float lrow = p.lse2[rowstat];
+  float delta = p.fuse_delta ? 0.f : p.delta[rowstat];
+  // fully masked row (lse2 = -inf) or row past T: P = 0
+  const float neg_lse = (!qvalid || lrow == -INFINITY) ? -INFINITY : -lrow;
 
   const __bf16* kbase = p.k + b * p.k_sb + hk * p.k_sh;
   const __bf16* vbase = p.v + b * p.v_sb + hk * p.v_sh;
@@ -380,21 +409,6 @@ __global__ __launch_bounds__(kThreads, 2) void bwd_dq_kernel(BwdParams p) {
   koff[U::kPerWave] = unit_dma_offset<D>(U::kInsts - 1, p.k_st, lane);
   voff[U::kPerWave] = unit_dma_offset<D>(U::kInsts - 1, p.v_st, lane);
 
-  const size_t row = (size_t)mb * nt + qt;
-  const int npart = uniform(p.m.kv_num[row]);
-  const int nfull = uniform(p.m.full_kv_num[row]);
-  const int ntiles = npart + nfull;
-  const int32_t* pidx = p.m.kv_idx + row * nt;
-  const int32_t* fidx = p.m.full_kv_idx + row * nt;
-  const uint32_t* bits_row = p.m.tile_bits + (size_t)p.m.kv_bits_off[row] * kTileBitsWords;
-
-  // KV tile indices of the row, 64 iterations per chunk (lane j: iteration
-  // 64 * chunk + j), read back with readlane.
-  auto load_chunk = [&](int chunk) {
-    const int it = 64 * chunk + lane;
-    return it < npart ? pidx[it] : (it < ntiles ? fidx[it - npart] : 0);
-  };
-  int tiles_v = load_chunk(0);
   auto tile_of = [&](int it) { return __builtin_amdgcn_readlane(tiles_v, it & 63); };
   const auto krs = slice_rsrc(kbase, p.k_st, T, D);
   const auto vrs = slice_rsrc(vbase, p.v_st, T, D);
@@ -468,6 +482,17 @@ __global__ __launch_bounds__(kThreads, 2) void bwd_dq_kernel(BwdParams p) {
     load_half(k_lo, v_lo, k0_next);
     if (npart > 0) load_bits(0);
   }
+  if (p.fuse_delta) {
+    // While the first K/V half is in flight: the two lane halves of a row
+    // each sum half its products; written once per row for dK/dV.
+    float acc = 0.f;
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc = fmaf((float)of[s][j], (float)dof[s][j], acc);
+    delta = halves_sum(acc);
+    if (qvalid && g == 0) p.delta[rowstat] = delta;
+  }
   for (int it = 0; it < ntiles; ++it) {
     const bool partial = it < npart;
     const int k0 = k0_next;
@@ -520,6 +545,7 @@ BwdParams make_bwd_params(const TensorView& q, const TensorView& k, const Tensor
   p.B = dims.B; p.Hq = dims.Hq; p.Hkv = dims.Hkv; p.T = dims.T;
   p.scale = dims.scale;
   p.scale_log2 = dims.scale * kLog2e;
+  p.fuse_delta = 0;
   p.m = mask;
   return p;
 }
@@ -546,10 +572,12 @@ hipError_t launch_attn_bwd_phase(int phase, const TensorView& q, const TensorVie
     const dim3 grid(dims.Hkv, nt, dims.B);
     if (d64) hipLaunchKernelGGL(bwd_dkdv_kernel<64>, grid, dim3(kDkdvThreads), 0, stream, p);
     else hipLaunchKernelGGL(bwd_dkdv_kernel<128>, grid, dim3(kDkdvThreads), 0, stream, p);
-  } else {
+  } else {  // kBwdDq, kBwdDqDelta
+    BwdParams pq = p;
+    pq.fuse_delta = phase == kBwdDqDelta;
     const dim3 grid(dims.Hq, nt, dims.B);
-    if (d64) hipLaunchKernelGGL(bwd_dq_kernel<64>, grid, dim3(kThreads), 0, stream, p);
-    else hipLaunchKernelGGL(bwd_dq_kernel<128>, grid, dim3(kThreads), 0, stream, p);
+    if (d64) hipLaunchKernelGGL(bwd_dq_kernel<64>, grid, dim3(kThreads), 0, stream, pq);
+    else hipLaunchKernelGGL(bwd_dq_kernel<128>, grid, dim3(kThreads), 0, stream, pq);
   }
   return hipGetLastError();
 }

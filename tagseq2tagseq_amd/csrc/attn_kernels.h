@@ -69,7 +69,8 @@ hipError_t launch_attn_fwd_bf16(const TensorView& q, const TensorView& k, const 
                                 const TensorView& o, float* lse2, const AttnDims& dims,
                                 const MaskTables& mask, hipStream_t stream);
 
-enum BwdPhase { kBwdDelta = 0, kBwdDkDv = 1, kBwdDq = 2 };
+// kBwdDqDelta: dQ that also computes and writes Delta (run before dK/dV).
+enum BwdPhase { kBwdDelta = 0, kBwdDkDv = 1, kBwdDq = 2, kBwdDqDelta = 3 };
 
 // One backward phase.  Views a phase does not read may be empty (delta: o,
 // dout; dkdv: q, k, v, dout, lse2, delta, dk, dv; dq: q, k, v, dout, lse2,

@@ -234,7 +234,7 @@ int t2t_attn_bwd(const t2t_tensor* q, const t2t_tensor* k, const t2t_tensor* v,
                  const t2t_tensor* dv, int32_t B, int32_t Hq, int32_t Hkv, int32_t T,
                  int32_t D, int32_t dtype, float scale, const t2t_block_mask* mask,
                  void* stream) {
-  // Validate every argument of the three phases before launching any of them.
+  // Validate every argument before launching anything.
   int rc = check_dims(B, Hq, Hkv, T, D, dtype);
   if (rc) return rc;
   if (B == 0 || Hq == 0 || T == 0) return T2T_OK;
@@ -244,13 +244,18 @@ int t2t_attn_bwd(const t2t_tensor* q, const t2t_tensor* k, const t2t_tensor* v,
   if (!lse2 || !delta) return fail(T2T_EINVAL, "lse2/delta is NULL");
   rc = check_mask(mask, B, T, true, true);
   if (rc) return rc;
-  rc = t2t_attn_bwd_preprocess(o, dout, delta, B, Hq, T, D, dtype, stream);
+  // dQ first: it computes each row's Delta = rowsum(O * dO) from the dO rows
+  // it holds and writes it for dK/dV, so no separate Delta launch is needed.
+  t2t::AttnDims dims{B, Hq, Hkv, T, D, scale};
+  rc = hip_status(t2t::launch_attn_bwd_phase(t2t::kBwdDqDelta, as_view(q), as_view(k),
+                                             as_view(v), as_view(o), as_view(dout), lse2, delta,
+                                             as_view(dq), t2t::TensorView{nullptr, 0, 0, 0},
+                                             t2t::TensorView{nullptr, 0, 0, 0}, dims,
+                                             as_tables(mask), static_cast<hipStream_t>(stream)),
+                  "t2t_attn_bwd dQ launch");
   if (rc) return rc;
-  rc = t2t_attn_bwd_dkdv(q, k, v, dout, lse2, delta, dk, dv, B, Hq, Hkv, T, D, dtype, scale,
-                         mask, stream);
-  if (rc) return rc;
-  return t2t_attn_bwd_dq(q, k, v, dout, lse2, delta, dq, B, Hq, Hkv, T, D, dtype, scale, mask,
-                         stream);
+  return t2t_attn_bwd_dkdv(q, k, v, dout, lse2, delta, dk, dv, B, Hq, Hkv, T, D, dtype, scale,
+                           mask, stream);
 }
 
 namespace {
