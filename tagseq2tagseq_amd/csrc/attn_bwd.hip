@@ -79,6 +79,22 @@ __global__ __launch_bounds__(kThreads) void bwd_delta_kernel(BwdParams p) {
   if (rowid < nrows && sub == 0) p.delta[rowid] = acc;
 }
 
+// P and dS of a mixed dK/dV block in place (sacc -> P, dpacc -> dS) for a
+// lane whose bitmap word, shifted right by its lane group, is wg: P of a
+// masked pair is cleared with the pair's sign-extended mask bit.
+template <int I = 0>
+__device__ __forceinline__ void keep_masked(f32x16& sacc, uint32_t wg, const float* lu,
+                                            const float* dlu, f32x16& dpacc, float c, int g) {
+  if constexpr (I < 16) {
+    const int qr = acc_row(I, g);
+    const float e = fast_exp2(fmaf(sacc[I], c, -lu[qr]));
+    const float pv = __int_as_float(__float_as_int(e) & sbfe1_c<acc_tok_bit(I)>(wg));
+    sacc[I] = pv;
+    dpacc[I] = pv * (dpacc[I] - dlu[qr]);
+    keep_masked<I + 1>(sacc, wg, lu, dlu, dpacc, c, g);
+  }
+}
+
 constexpr int kDkdvWaves = 8;  // 4 key groups x 2 query blocks
 constexpr int kDkdvThreads = 64 * kDkdvWaves;
 
@@ -208,7 +224,7 @@ __global__ __launch_bounds__(kDkdvThreads, 1) void bwd_dkdv_kernel(BwdParams p) 
     if (partial && __ballot(w != 0u) == 0ull) return;
     const bool mixed = partial && __ballot(w != ~0u) != 0ull;
     const int rb = 32 * qh;
-    f32x16 sacc = mixed ? mask_bias(~(w >> g)) : f32x16{};
+    f32x16 sacc = f32x16{};
     f32x16 dpacc = f32x16{};
     __builtin_amdgcn_s_setprio(1);  // MFMA runs at raised wave priority
 #pragma unroll
@@ -221,15 +237,21 @@ __global__ __launch_bounds__(kDkdvThreads, 1) void bwd_dkdv_kernel(BwdParams p) 
       dpacc = mfma32(da, vb, dpacc);
     }
     __builtin_amdgcn_s_setprio(0);
+    // Masked pairs of a mixed block: P is cleared by and-ing its bits with
+    // the pair's sign-extended mask bit, after the exponential.  Only a
+    // mixed block can hold a fully masked row (LSE = -inf), whose
+    // exp2(+inf) is cleared the same way; every other row has a finite LSE.
+    if (mixed) {
+      const uint32_t wg = w >> g;
+      keep_masked(sacc, wg, lu + rb, dlu + rb, dpacc, c, g);
+    } else {
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int qr = rb + acc_row(i, g);
-      // A fully masked row has LSE = -inf and only -inf scores; clamping
-      // keeps exp2(-inf - lse) at 0 instead of NaN.
-      const float lse = fmaxf(lu[qr], -3.402823466e38f);
-      const float pv = fast_exp2(fmaf(sacc[i], c, -lse));
-      sacc[i] = pv;                                 // P
-      dpacc[i] = pv * (dpacc[i] - dlu[qr]);         // dS
+      for (int i = 0; i < 16; ++i) {
+        const int qr = rb + acc_row(i, g);
+        const float pv = fast_exp2(fmaf(sacc[i], c, -lu[qr]));
+        sacc[i] = pv;                                 // P
+        dpacc[i] = pv * (dpacc[i] - dlu[qr]);         // dS
+      }
     }
     // dV^T += dO^T P, dK^T += Q^T dS (contraction over the 32 queries).
     __builtin_amdgcn_s_setprio(1);
