@@ -127,7 +127,10 @@ __global__ __launch_bounds__(kDkdvThreads, 1) void bwd_dkdv_kernel(BwdParams p) 
 
   const int hk = blockIdx.x, b = blockIdx.z;
   const int tid = threadIdx.x, wave = uniform(tid >> 6), lane = tid & 63;
-  const int kw = wave & 3, qh = wave >> 2;
+  // Waves w and w + 4 share a SIMD; pairing key groups two apart there keeps
+  // both busy on tiles whose upper key groups are masked for a whole half
+  // (the causal diagonal), where the same key group would leave it idle.
+  const int qh = wave >> 2, kw = (wave + 2 * qh) & 3;
   const int g = lane >> 5, n = lane & 31;
   const int G = p.Hq / p.Hkv;
   const int mb = p.m.Bm > 1 ? b : 0;
