@@ -42,6 +42,7 @@ from tagseq2tagseq_amd.mask_creators import TokenLists  # noqa: E402
 METRIC = "masked attn fwd+bwd useful TFLOP/s + % bf16 MFMA peak, cross_doc_link T=16k"
 PEAK_BF16_TFLOPS = 2516.6   # MI355X dense bf16 MFMA: 256 CU x 2.4 GHz x 4096 FLOP/clk
 PEAK_HBM_GBS = 8000.0
+PEAK_F32_TFLOPS = 157.3     # MI355X dense fp32 MFMA
 
 WORKLOAD_NAMES = {
     2: "doc_causal fwd+bwd bf16 B2 H12 T8192 D64 (configs[1])",
@@ -372,6 +373,92 @@ def decode_bench(args, dev):
     }))
 
 
+def config1_bench(args, dev):
+    """doc_causal forward only, float32, B1 H4 T1024 D64 -- the
+    reference's CPU-runnable case.  A step = per-token inputs from the span
+    lists + metadata pass + float32 forward; value = 4 D N_pairs H / step time
+    (forward-only useful FLOPs).  Next to it, the reference's own CPU path on
+    the same inputs (torch eager create_block_mask + flex_attention forward in
+    float32, every head) and the torch.compile(flex_attention) CPU forward."""
+    from oracle.mask_oracle import torch_mask_mod
+    from torch.nn.attention.flex_attention import create_block_mask
+    from torch.nn.attention.flex_attention import flex_attention as torch_flex
+    c = synth.CONFIGS[1]
+    B, Hq, Hkv, T, D = c["B"], c["Hq"], c["Hkv"], c["T"], c["D"]
+    rows = synth.config_rows(1, seed=args.seed)
+    rows_np = [per_token_arrays(r) for r in rows]
+    doc = torch.from_numpy(rows_np[0][0]).to(dev)[None]
+    n_pairs = count_pairs(doc[0], None, None)
+    useful = 4.0 * D * n_pairs * Hq
+    g = torch.Generator().manual_seed(args.seed)
+    qc, kc, vc = (torch.randn(B, h, T, D, generator=g) for h in (Hq, Hkv, Hkv))
+    q, k, v = (t.to(dev) for t in (qc, kc, vc))
+    scale = 1.0 / math.sqrt(D)
+    lists = TokenLists(T, [r.spans for r in rows], dev)
+
+    def step():
+        bm = build_block_mask(*lists.build())
+        return attn_fwd(q, k, v, bm, scale)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(args.steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / args.steps
+    bm = build_block_mask(*lists.build())
+    t_fwd = time_launches(lambda: attn_fwd(q, k, v, bm, scale), args.reps)
+    achieved = useful / (t_fwd * 1e-3) / 1e12
+    result = {
+        "metric": "masked attn fwd useful TFLOP/s, doc_causal float32 T=1k (configs[0])",
+        "value": round(useful / (ms * 1e-3) / 1e12, 4), "unit": "TFLOP/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (seeded packed documents, Q/K/V ~ N(0,1))",
+        "config": {"workload": "doc_causal fwd float32 B1 H4 T1024 D64 (configs[0])", "B": B,
+                   "Hq": Hq, "Hkv": Hkv, "T": T, "D": D, "seed": args.seed,
+                   "n_docs": [r.n_docs for r in rows], "n_pairs": n_pairs},
+        "roofline": {"bound": "mfma", "kernel": "attn_fwd_f32_kernel", "achieved": round(achieved, 3),
+                     "peak": PEAK_F32_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(achieved / PEAK_F32_TFLOPS, 4), "traffic": None},
+        "kernels_ms": {"attn_fwd_f32_kernel": round(t_fwd, 4)},
+    }
+    if not args.no_cpu_baseline:
+        torch.set_num_threads(args.cpu_threads)
+        mod = torch_mask_mod(torch.from_numpy(rows_np[0][0]), None, None)
+        t0 = time.perf_counter()
+        cbm = create_block_mask(mod, None, None, T, T, device="cpu")
+        out = torch_flex(qc, kc, vc, block_mask=cbm)
+        t_eager = time.perf_counter() - t0
+        # same inputs: the GPU float32 forward against the reference's CPU output
+        got = attn_fwd(q, k, v, bm, scale)[0].float().cpu()
+        max_err = float((got - out).abs().max())
+        result["cpu_baseline"] = {
+            "value": round(useful / t_eager / 1e12, 6), "unit": "TFLOP/s",
+            "cores": args.cpu_threads, "kind": "reference",
+            "sample": (f"torch {torch.__version__} eager create_block_mask + flex_attention "
+                       f"forward, float32, all {Hq} heads, on CPU ({t_eager:.3f} s)"),
+            "max_abs_diff_vs_gpu": max_err,
+        }
+        try:
+            cf = torch.compile(torch_flex)
+            cf(qc, kc, vc, block_mask=cbm)  # compile
+            t0 = time.perf_counter()
+            cf(qc, kc, vc, block_mask=cbm)
+            t_comp = time.perf_counter() - t0
+            result["cpu_compiled_fwd"] = {"s": round(t_comp, 4),
+                                          "TFLOPs": round(useful / t_comp / 1e12, 6),
+                                          "sample": "torch.compile(flex_attention) forward on CPU, "
+                                                    "block mask prebuilt, second call"}
+        except Exception as e:  # inductor's CPU path needs a host C++ toolchain
+            result["cpu_compiled_fwd"] = {"error": f"{type(e).__name__}: {str(e)[:200]}"}
+    print(json.dumps(result))
+
+
 def backbone_step(args, dev):
     """one training step (mask creation from the device-resident
     span / link lists, embedding, 12 layers, RMSNorm, tied linear + CE loss,
@@ -434,9 +521,10 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", type=int, default=3, choices=[2, 3, 4, 5],
+    ap.add_argument("--config", type=int, default=3, choices=[1, 2, 3, 4, 5],
                     help="3 (default): the metric's workload; 2, 4: other attention "
-                         "workloads; 5: 12-layer backbone training step (tokens/s)")
+                         "workloads; 1: float32 forward-only case; 5: 12-layer backbone "
+                         "training step (tokens/s)")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--reps", type=int, default=20, help="launches per per-kernel timing")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -468,6 +556,9 @@ def main():
         return
     if args.config == 5:
         backbone_step(args, dev)
+        return
+    if args.config == 1:
+        config1_bench(args, dev)
         return
 
     if args.copy_calibration:

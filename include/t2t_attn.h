@@ -32,6 +32,7 @@ extern "C" {
 #define T2T_EHIP (-3)         /* a HIP launch or runtime call failed */
 
 #define T2T_DTYPE_BF16 0
+#define T2T_DTYPE_F32 1
 
 #define T2T_TILE 128   /* BlockMask tile edge (torch/nn/attention/flex_attention.py:395) */
 #define T2T_MAX_WORDS 8
@@ -145,7 +146,9 @@ int t2t_mask_meta(const int32_t *doc, const uint64_t *q_bits, const uint64_t *kv
  * q [B,Hq,T,D], k/v [B,Hkv,T,D], o [B,Hq,T,D] (dtype), lse2 float[B][Hq][T]
  * (contiguous) = log2-sum-exp2 of the masked row of (Q K^T * scale * log2 e);
  * natural-log LSE = lse2 * ln 2; fully masked rows give o = 0, lse2 = -inf.
- * Supported: dtype T2T_DTYPE_BF16, D in {64, 128}, Hq % Hkv == 0.
+ * Supported: dtype T2T_DTYPE_BF16 or T2T_DTYPE_F32 (q, k, v, o all of that
+ * type; float32 is computed in float32 throughout), D in {64, 128},
+ * Hq % Hkv == 0.
  */
 int t2t_attn_fwd(const t2t_tensor *q, const t2t_tensor *k, const t2t_tensor *v,
                  const t2t_tensor *o, float *lse2, int32_t B, int32_t Hq, int32_t Hkv,
@@ -157,7 +160,9 @@ int t2t_attn_fwd(const t2t_tensor *q, const t2t_tensor *k, const t2t_tensor *v,
  * FlexAttentionAutogradOp.backward (torch/_higher_order_ops/flex_attention.py:689-767;
  * eager arithmetic sdpa_dense_backward :825-994).
  * delta: float[B][Hq][T] workspace, overwritten with rowsum(O * dO) by the dQ
- * launch (which runs first and computes it) and read by dK/dV.  dq like q; dk/dv like k/v
+ * launch (which runs first and computes it) and read by dK/dV.  dtype
+ * T2T_DTYPE_BF16 or T2T_DTYPE_F32 (all tensors of that type; float32 is
+ * computed in float32 throughout).  dq like q; dk/dv like k/v
  * (summed over each GQA group, written, not accumulated).  No atomics: the
  * result is bitwise deterministic.
  */
@@ -171,7 +176,8 @@ int t2t_attn_bwd(const t2t_tensor *q, const t2t_tensor *k, const t2t_tensor *v,
 /*
  * The backward's phases, callable separately (for example to run dK/dV and
  * dQ on two streams once Delta is ready; t2t_attn_bwd itself runs a dQ that
- * also writes Delta, then dK/dV).  Same conventions:
+ * also writes Delta, then dK/dV).  bf16 only (float32 runs as one
+ * t2t_attn_bwd call).  Same conventions:
  *   preprocess: delta[b][h][t] = sum_d o * dout  (sdpa_dense_backward :910-914)
  *   dkdv:       dk, dv  (KV-tile-major, walks q_num/q_idx + full_q_*)
  *   dq:         dq      (Q-tile-major, walks kv_num/kv_idx + full_kv_*)

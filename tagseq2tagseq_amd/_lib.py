@@ -16,6 +16,7 @@ HEADER_PATH = os.path.join(os.path.dirname(HERE), "include", "t2t_attn.h")
 
 T2T_OK = 0
 T2T_DTYPE_BF16 = 0
+T2T_DTYPE_F32 = 1
 TILE = 128
 MAX_WORDS = 8
 TILE_BITS_WORDS = 1024  # uint32 per tile bitmap slot ([2][128][4])

@@ -37,7 +37,7 @@ from typing import List, Tuple
 from .block_mask import T2TBlockMask, tables_c_struct
 
 LN2 = math.log(2.0)
-_DTYPE_CODES = {torch.bfloat16: _lib.T2T_DTYPE_BF16}
+_DTYPE_CODES = {torch.bfloat16: _lib.T2T_DTYPE_BF16, torch.float32: _lib.T2T_DTYPE_F32}
 
 
 def _stream_ptr(t: torch.Tensor) -> ctypes.c_void_p:
@@ -64,7 +64,7 @@ def _validate(q, k, v, block_mask, enable_gqa):
     if not (q.dtype == k.dtype == v.dtype):
         raise ValueError(f"dtype mismatch: {q.dtype}, {k.dtype}, {v.dtype}")
     if q.dtype not in _DTYPE_CODES:
-        raise NotImplementedError(f"dtype {q.dtype} is not supported (bfloat16 only)")
+        raise NotImplementedError(f"dtype {q.dtype} is not supported (bfloat16 or float32)")
     if not (q.is_cuda and k.is_cuda and v.is_cuda):
         raise RuntimeError("the masked-attention kernels need ROCm GPU tensors")
     B, Hq, T, D = q.shape

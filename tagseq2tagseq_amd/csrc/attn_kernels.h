@@ -69,6 +69,18 @@ hipError_t launch_attn_fwd_bf16(const TensorView& q, const TensorView& k, const 
                                 const TensorView& o, float* lse2, const AttnDims& dims,
                                 const MaskTables& mask, hipStream_t stream);
 
+// Float32 q / k / v / o (D in {64, 128}); same tables and LSE convention.
+hipError_t launch_attn_fwd_f32(const TensorView& q, const TensorView& k, const TensorView& v,
+                               const TensorView& o, float* lse2, const AttnDims& dims,
+                               const MaskTables& mask, hipStream_t stream);
+
+// Whole float32 backward: dQ (writing Delta), then dK/dV.
+hipError_t launch_attn_bwd_f32(const TensorView& q, const TensorView& k, const TensorView& v,
+                               const TensorView& o, const TensorView& dout, const float* lse2,
+                               float* delta, const TensorView& dq, const TensorView& dk,
+                               const TensorView& dv, const AttnDims& dims, const MaskTables& mask,
+                               hipStream_t stream);
+
 // kBwdDqDelta: dQ that also computes and writes Delta (run before dK/dV).
 enum BwdPhase { kBwdDelta = 0, kBwdDkDv = 1, kBwdDq = 2, kBwdDqDelta = 3 };
 

@@ -27,12 +27,16 @@ int hip_status(hipError_t e, const char* what) {
 // [T, D] slice, extended by one 128-row tile, spans less than 2 GiB, since the
 // kernels address a slice through a buffer resource with 31-bit byte offsets
 // (a tile starting at or past T is addressed, and reads as zeros).
-bool view_ok(const t2t_tensor* t, int T, int D) {
+// A [B, H, T, D] view of elements of `esize` bytes: 16-byte aligned base and
+// strides, and one (b, h) slice (plus a tile of padding rows) under 2 GiB so
+// that 32-bit buffer offsets reach it.
+bool view_ok(const t2t_tensor* t, int T, int D, int esize = 2) {
+  const int64_t align = 16 / esize;
   if (!(t && t->data && t->stride_b >= 0 && t->stride_h >= 0 && t->stride_t > 0 &&
-        (reinterpret_cast<uintptr_t>(t->data) % 16) == 0 && (t->stride_t % 8) == 0 &&
-        (t->stride_h % 8) == 0 && (t->stride_b % 8) == 0))
+        (reinterpret_cast<uintptr_t>(t->data) % 16) == 0 && (t->stride_t % align) == 0 &&
+        (t->stride_h % align) == 0 && (t->stride_b % align) == 0))
     return false;
-  const int64_t span_bytes = ((int64_t)T + t2t::kTile) * t->stride_t * 2 + (int64_t)D * 2;
+  const int64_t span_bytes = (((int64_t)T + t2t::kTile) * t->stride_t + (int64_t)D) * esize;
   return span_bytes <= 0x7fffffffLL - 16;
 }
 
@@ -71,11 +75,12 @@ t2t::MaskTables as_tables(const t2t_block_mask* m) {
   return t;
 }
 
-int check_dims(int B, int Hq, int Hkv, int T, int D, int dtype) {
+int check_dims(int B, int Hq, int Hkv, int T, int D, int dtype, bool f32_ok = false) {
   if (B < 0 || Hq < 0 || Hkv <= 0 || T < 0) return fail(T2T_EINVAL, "negative size");
   if (Hq % Hkv != 0)
     return fail(T2T_EINVAL, "Hq=%d must be a multiple of Hkv=%d (GQA)", Hq, Hkv);
-  if (dtype != T2T_DTYPE_BF16) return fail(T2T_EUNSUPPORTED, "dtype %d not supported", dtype);
+  if (!(dtype == T2T_DTYPE_BF16 || (f32_ok && dtype == T2T_DTYPE_F32)))
+    return fail(T2T_EUNSUPPORTED, "dtype %d not supported here", dtype);
   if (D != 64 && D != 128) return fail(T2T_EUNSUPPORTED, "head dim D=%d not in {64, 128}", D);
   return T2T_OK;
 }
@@ -150,18 +155,24 @@ int t2t_attn_fwd(const t2t_tensor* q, const t2t_tensor* k, const t2t_tensor* v,
                  const t2t_tensor* o, float* lse2, int32_t B, int32_t Hq, int32_t Hkv,
                  int32_t T, int32_t D, int32_t dtype, float scale, const t2t_block_mask* mask,
                  void* stream) {
-  int rc = check_dims(B, Hq, Hkv, T, D, dtype);
+  int rc = check_dims(B, Hq, Hkv, T, D, dtype, true);
   if (rc) return rc;
   if (B == 0 || Hq == 0 || T == 0) return T2T_OK;
-  if (!view_ok(q, T, D) || !view_ok(k, T, D) || !view_ok(v, T, D) || !view_ok(o, T, D))
+  const int es = dtype == T2T_DTYPE_F32 ? 4 : 2;
+  if (!view_ok(q, T, D, es) || !view_ok(k, T, D, es) || !view_ok(v, T, D, es) ||
+      !view_ok(o, T, D, es))
     return fail(T2T_EINVAL, "q/k/v/o view invalid (NULL, misaligned, bad stride or slice >= 2 GiB)");
   if (!lse2) return fail(T2T_EINVAL, "lse2 is NULL");
   rc = check_mask(mask, B, T, true, false);
   if (rc) return rc;
   t2t::AttnDims dims{B, Hq, Hkv, T, D, scale};
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  if (dtype == T2T_DTYPE_F32)
+    return hip_status(t2t::launch_attn_fwd_f32(as_view(q), as_view(k), as_view(v), as_view(o),
+                                               lse2, dims, as_tables(mask), st),
+                      "t2t_attn_fwd launch");
   return hip_status(t2t::launch_attn_fwd_bf16(as_view(q), as_view(k), as_view(v), as_view(o),
-                                              lse2, dims, as_tables(mask),
-                                              static_cast<hipStream_t>(stream)),
+                                              lse2, dims, as_tables(mask), st),
                     "t2t_attn_fwd launch");
 }
 
@@ -235,18 +246,26 @@ int t2t_attn_bwd(const t2t_tensor* q, const t2t_tensor* k, const t2t_tensor* v,
                  int32_t D, int32_t dtype, float scale, const t2t_block_mask* mask,
                  void* stream) {
   // Validate every argument before launching anything.
-  int rc = check_dims(B, Hq, Hkv, T, D, dtype);
+  int rc = check_dims(B, Hq, Hkv, T, D, dtype, true);
   if (rc) return rc;
   if (B == 0 || Hq == 0 || T == 0) return T2T_OK;
-  if (!view_ok(q, T, D) || !view_ok(k, T, D) || !view_ok(v, T, D) || !view_ok(o, T, D) || !view_ok(dout, T, D) ||
-      !view_ok(dq, T, D) || !view_ok(dk, T, D) || !view_ok(dv, T, D))
+  const int es = dtype == T2T_DTYPE_F32 ? 4 : 2;
+  if (!view_ok(q, T, D, es) || !view_ok(k, T, D, es) || !view_ok(v, T, D, es) ||
+      !view_ok(o, T, D, es) || !view_ok(dout, T, D, es) || !view_ok(dq, T, D, es) ||
+      !view_ok(dk, T, D, es) || !view_ok(dv, T, D, es))
     return fail(T2T_EINVAL, "tensor view invalid (NULL, misaligned, bad stride or slice >= 2 GiB)");
   if (!lse2 || !delta) return fail(T2T_EINVAL, "lse2/delta is NULL");
   rc = check_mask(mask, B, T, true, true);
   if (rc) return rc;
+  t2t::AttnDims dims{B, Hq, Hkv, T, D, scale};
+  if (dtype == T2T_DTYPE_F32)
+    return hip_status(t2t::launch_attn_bwd_f32(as_view(q), as_view(k), as_view(v), as_view(o),
+                                               as_view(dout), lse2, delta, as_view(dq),
+                                               as_view(dk), as_view(dv), dims, as_tables(mask),
+                                               static_cast<hipStream_t>(stream)),
+                      "t2t_attn_bwd launch");
   // dQ first: it computes each row's Delta = rowsum(O * dO) from the dO rows
   // it holds and writes it for dK/dV, so no separate Delta launch is needed.
-  t2t::AttnDims dims{B, Hq, Hkv, T, D, scale};
   rc = hip_status(t2t::launch_attn_bwd_phase(t2t::kBwdDqDelta, as_view(q), as_view(k),
                                              as_view(v), as_view(o), as_view(dout), lse2, delta,
                                              as_view(dq), t2t::TensorView{nullptr, 0, 0, 0},

@@ -143,10 +143,30 @@ class QKVRopeFn(torch.autograd.Function):
         return _qkv_rope_bwd_impl(dq, dk, dv, cos, sin, ctx.pos0), None, None, None, None
 
 
+def qkv_rope_torch(qkv: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, num_heads: int,
+                   pos0: int = 0):
+    """The same split and rotation composed from torch ops in qkv's dtype, for
+    modules whose dtype the prologue kernel does not take (float32)."""
+    B, T, D = _split_dims(qkv, num_heads)
+    x = qkv.view(B, T, 3, num_heads, D).permute(2, 0, 3, 1, 4)  # [3, B, H, T, D]
+    c = cos[pos0:pos0 + T].to(qkv.dtype)
+    s = sin[pos0:pos0 + T].to(qkv.dtype)
+    h = D // 2
+
+    def rot(t):
+        t1, t2 = t[..., :h], t[..., h:]
+        return torch.cat((t1 * c + t2 * s, t2 * c - t1 * s), dim=-1)
+
+    return rot(x[0]).contiguous(), rot(x[1]).contiguous(), x[2].contiguous()
+
+
 def qkv_rope(qkv: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, num_heads: int,
              pos0: int = 0):
     """Split qkv [B, T, 3 C] into rotated q, k and v, each [B, H, T, D]
-    (contiguous), with positions pos0 .. pos0 + T - 1 (table rows)."""
+    (contiguous), with positions pos0 .. pos0 + T - 1 (table rows).  bf16 runs
+    the kernel; float32 (module not cast to bf16) the torch composition."""
+    if qkv.dtype == torch.float32:
+        return qkv_rope_torch(qkv, cos, sin, num_heads, pos0)
     if torch.compiler.is_compiling():
         return qkv_rope_op(qkv, cos, sin, int(num_heads), int(pos0))
     return QKVRopeFn.apply(qkv, cos, sin, int(num_heads), int(pos0))

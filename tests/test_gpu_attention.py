@@ -2,7 +2,8 @@
 
 Small cases: against the float64 CPU oracle (oracle/attn_oracle.py).
 Full-size configs: against a chunked fp32 torch reference on the GPU over a
-subset of heads.  bf16 tolerance 2e-2 (abs and rel), the north-star bound.
+subset of heads.  bf16 tolerance 2e-2 (abs and rel), float32 1e-4: the
+north-star bounds.
 """
 import math
 
@@ -21,6 +22,7 @@ from tests.helpers import (assert_close, random_row, row_arrays, to_dev_words,
 pytestmark = pytest.mark.gpu
 
 ATOL = RTOL = 2e-2
+F32_TOL = 1e-4
 
 
 def _mask_from_rows(rows_np, device):
@@ -41,24 +43,29 @@ def _inputs(B, Hq, Hkv, T, D, seed, device, dtype=torch.bfloat16):
     return [t.to(device) for t in (q, k, v, do)]
 
 
-def _oracle_check(rows_np, B, Hq, Hkv, T, D, seed, device, bwd=True):
+def _oracle_check(rows_np, B, Hq, Hkv, T, D, seed, device, bwd=True, dtype=torch.bfloat16):
+    """Kernels vs the float64 oracle on the same inputs: 2e-2 (abs and rel)
+    for bf16, 1e-4 for float32; LSE 1e-3 / 1e-4."""
+    tol, lse_tol = (ATOL, 1e-3) if dtype == torch.bfloat16 else (F32_TOL, F32_TOL)
     bm = _mask_from_rows(rows_np, device)
-    q, k, v, do = _inputs(B, Hq, Hkv, T, D, seed, device)
+    q, k, v, do = _inputs(B, Hq, Hkv, T, D, seed, device, dtype)
     q.requires_grad_(True); k.requires_grad_(True); v.requires_grad_(True)
     out, lse = flex_attention(q, k, v, block_mask=bm, enable_gqa=Hq != Hkv, return_lse=True)
+    assert out.dtype == dtype
     dense = np.stack([mo.dense_mask(*r) for r in rows_np])
     qn, kn, vn, don = (t.detach().float().cpu().numpy() for t in (q, k, v, do))
     o_ref, lse_ref = ao.attention_fwd(qn, kn, vn, dense)
-    label = f"B{B} H{Hq}/{Hkv} T{T} D{D}"
-    assert_close(out.detach(), torch.from_numpy(o_ref), ATOL, RTOL, f"out {label}")
-    assert_close(lse.detach(), torch.from_numpy(lse_ref), 1e-3, 1e-3, f"lse {label}")
+    label = f"B{B} H{Hq}/{Hkv} T{T} D{D} {dtype}"
+    assert_close(out.detach(), torch.from_numpy(o_ref), tol, tol, f"out {label}")
+    assert_close(lse.detach(), torch.from_numpy(lse_ref), lse_tol, lse_tol, f"lse {label}")
     if not bwd:
         return
     out.backward(do)
     dq_ref, dk_ref, dv_ref = ao.attention_bwd(qn, kn, vn, o_ref, don, lse_ref, dense)
-    assert_close(q.grad, torch.from_numpy(dq_ref), ATOL, RTOL, f"dq {label}")
-    assert_close(k.grad, torch.from_numpy(dk_ref), ATOL, RTOL, f"dk {label}")
-    assert_close(v.grad, torch.from_numpy(dv_ref), ATOL, RTOL, f"dv {label}")
+    assert q.grad.dtype == k.grad.dtype == v.grad.dtype == dtype
+    assert_close(q.grad, torch.from_numpy(dq_ref), tol, tol, f"dq {label}")
+    assert_close(k.grad, torch.from_numpy(dk_ref), tol, tol, f"dk {label}")
+    assert_close(v.grad, torch.from_numpy(dv_ref), tol, tol, f"dv {label}")
 
 
 @pytest.mark.parametrize("D", [64, 128])
@@ -89,6 +96,29 @@ def test_ragged_uncovered_tokens(gpu_device):
 def test_config1_shape_bf16(gpu_device):
     rows = [row_arrays(r) for r in synth.config_rows(1, seed=0)]
     _oracle_check(rows, 1, 4, 4, 1024, 64, seed=0, device=gpu_device)
+
+
+def test_config1_f32(gpu_device):
+    """Config 1 as specified: float32 doc_causal B1 H4 T1024 D64 (forward,
+    plus the float32 backward on the same inputs)."""
+    rows = [row_arrays(r) for r in synth.config_rows(1, seed=0)]
+    _oracle_check(rows, 1, 4, 4, 1024, 64, seed=0, device=gpu_device, dtype=torch.float32)
+
+
+@pytest.mark.parametrize("D", [64, 128])
+def test_f32_doc_causal_and_cross_doc_link(D, gpu_device):
+    rows = [row_arrays(synth.lognormal_docs(384, 60.0, 1.0, 300, seed=D))]
+    _oracle_check(rows, 1, 2, 2, 384, D, seed=6, device=gpu_device, dtype=torch.float32)
+    rows = [row_arrays(synth.linked_lognormal_docs(512, 50.0, 1.0, 300, 0.3, seed=4))]
+    _oracle_check(rows, 1, 2, 2, 512, D, seed=7, device=gpu_device, dtype=torch.float32)
+
+
+def test_f32_gqa_batch_masks_and_ragged(gpu_device):
+    rng = np.random.default_rng(21)
+    rows = [random_row(384, rng, words=2, uncovered=True, max_doc=120) for _ in range(2)]
+    _oracle_check(rows, 2, 4, 2, 384, 64, seed=8, device=gpu_device, dtype=torch.float32)
+    rows = [random_row(333, rng, words=1, uncovered=True, max_doc=90)]
+    _oracle_check(rows, 1, 4, 1, 333, 128, seed=9, device=gpu_device, dtype=torch.float32)
 
 
 def test_backward_is_deterministic(gpu_device):

@@ -46,6 +46,30 @@ def test_layer_matches_dense_reference(n_embd, n_head, monkeypatch):
     assert_close(got, ref, 2e-2, 2e-2, "layer output")
 
 
+def test_float32_layer_forward_and_backward(monkeypatch):
+    """A Layer left in float32 runs the float32 attention kernels (and the
+    torch QKV rotation); output and input gradient against the same Layer
+    with fp32 dense attention, at the float32 bound 1e-4."""
+    T = 384
+    row = synth.linked_lognormal_docs(T, 90.0, 1.0, 384, 0.3, seed=5)
+    lists = TokenLists(T, [row.spans], DEV, words=row.words, link_rows=[row.link_rows])
+    bm = build_block_mask(*lists.build())
+    torch.manual_seed(1)
+    layer = Layer(256, 4, 0.0, T, False, 0.0).to(DEV)
+    x = torch.randn(1, T, 256, device=DEV)
+    g = torch.randn(1, T, 256, device=DEV)
+    xa = x.clone().requires_grad_(True)
+    got = layer(xa, bm)
+    got.backward(g)
+    monkeypatch.setattr(attn_mod, "flex_attention", _dense_flex(bm))
+    xb = x.clone().requires_grad_(True)
+    ref = layer(xb, bm)
+    ref.backward(g)
+    assert got.dtype == torch.float32
+    assert_close(got.detach(), ref.detach(), 1e-4, 1e-4, "float32 layer output")
+    assert_close(xa.grad, xb.grad, 1e-4, 1e-4, "float32 layer input gradient")
+
+
 def test_training_module_step():
     T = 1024
     row = synth.config_rows(3, seed=1, T=T)[0]

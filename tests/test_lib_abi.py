@@ -62,6 +62,33 @@ def test_fwd_rejects_bad_gqa_and_dtype():
 
 
 @no_gpu
+def test_float32_dtype_rules():
+    """float32 (dtype 1) is accepted by t2t_attn_fwd / t2t_attn_bwd with
+    4-byte-element alignment rules, and rejected by the separate phases."""
+    lib = _lib.lib()
+    m = _lib.T2TBlockMaskC()
+    f32_only = _lib.T2TTensor(0x1000, 0, 0, 132)  # row stride 132: 16-byte rows only as float32
+    rc = lib.t2t_attn_fwd(*[ctypes.byref(f32_only)] * 4, ctypes.c_void_p(0x1000), 1, 2, 2, 256,
+                          128, 0, 0.1, ctypes.byref(m), None)
+    assert rc == -1 and "view" in _err()
+    rc = lib.t2t_attn_fwd(*[ctypes.byref(f32_only)] * 4, ctypes.c_void_p(0x1000), 1, 2, 2, 256,
+                          128, 1, 0.1, None, None)
+    assert rc == -1 and "mask" in _err()  # the view passed; the NULL mask is what fails
+    rc = lib.t2t_attn_bwd(*[ctypes.byref(f32_only)] * 5, ctypes.c_void_p(0x1000),
+                          ctypes.c_void_p(0x1000), *[ctypes.byref(f32_only)] * 3,
+                          1, 2, 2, 256, 128, 1, 0.1, None, None)
+    assert rc == -1 and "mask" in _err()
+    v = _dummy_view()
+    rc = lib.t2t_attn_bwd_dkdv(*[ctypes.byref(v)] * 4, ctypes.c_void_p(0x1000),
+                               ctypes.c_void_p(0x1000), ctypes.byref(v), ctypes.byref(v),
+                               1, 2, 2, 256, 128, 1, 0.1, ctypes.byref(m), None)
+    assert rc == -2 and "dtype" in _err()
+    rc = lib.t2t_attn_bwd_preprocess(ctypes.byref(v), ctypes.byref(v), ctypes.c_void_p(0x1000),
+                                     1, 2, 256, 128, 1, None)
+    assert rc == -2 and "dtype" in _err()
+
+
+@no_gpu
 def test_bwd_rejects_null_mask():
     v = _dummy_view()
     rc = _lib.lib().t2t_attn_bwd(*[ctypes.byref(v)] * 5, ctypes.c_void_p(0x1000),
