@@ -715,8 +715,7 @@ def main():
         },
         # The step's backward is t2t_attn_bwd: dQ computing Delta itself, then
         # dK/dV (bwd_delta above is the separate-phase entry point's launch).
-        "attn_bwd_ms": {"t2t_attn_bwd (dQ+Delta, dK/dV)": round(t_bwd, 4),
-                        "dQ+Delta (difference)": round(t_bwd - t_dkdv, 4)},
+        "attn_bwd_ms": {"t2t_attn_bwd (dQ+Delta, dK/dV)": round(t_bwd, 4)},
         "mask_meta": {"us": round(t_meta * 1e3, 2), "bytes": int(meta_bytes),
                       "GBps": round(meta_bytes / (t_meta * 1e-3) / 1e9, 2)},
         "token_inputs": {"us": round(t_tok * 1e3, 2), "bytes": int(tok_bytes),
