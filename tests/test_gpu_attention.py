@@ -160,6 +160,29 @@ def test_full_size_against_torch_fp32(cfg, gpu_device):
         assert_close(v.grad[b, hk], ref["dv"][(b, hk)], ATOL, RTOL, f"cfg{cfg} dv b{b} hk{hk}")
 
 
+def test_max_size_T65536(gpu_device):
+    """The largest shape exercised: T = 65536 (512 tiles per side, 376
+    documents, 6 grant words, ~1 GB of tile-bitmap slots) with the config-4
+    generator, one GQA group (Hq 4 / Hkv 1, D 128) so dK/dV are complete;
+    every output and gradient row against the chunked fp32 torch reference."""
+    T, Hq, Hkv, D = 65536, 4, 1, 128
+    rows = [row_arrays(r) for r in synth.config_rows(4, seed=1, T=T)]
+    bm = _mask_from_rows(rows, gpu_device)
+    assert bm.num_tiles == T // 128
+    q, k, v, do = _inputs(1, Hq, Hkv, T, D, 11, gpu_device)
+    q.requires_grad_(True); k.requires_grad_(True); v.requires_grad_(True)
+    out = flex_attention(q, k, v, block_mask=bm, enable_gqa=True)
+    out.backward(do)
+    masks = [(torch.from_numpy(rows[0][0]).to(gpu_device), to_dev_words(rows[0][1], gpu_device),
+              to_dev_words(rows[0][2], gpu_device))]
+    ref = torch_ref_attention(q.detach(), k.detach(), v.detach(), do, masks)
+    for (b, h), o_ref in ref["o"].items():
+        assert_close(out[b, h].detach(), o_ref, ATOL, RTOL, f"T64k out h{h}")
+        assert_close(q.grad[b, h], ref["dq"][(b, h)], ATOL, RTOL, f"T64k dq h{h}")
+    assert_close(k.grad[0, 0], ref["dk"][(0, 0)], ATOL, RTOL, "T64k dk")
+    assert_close(v.grad[0, 0], ref["dv"][(0, 0)], ATOL, RTOL, "T64k dv")
+
+
 @pytest.mark.parametrize("name", ["cross_doc_link_T130_gqa", "doc_causal_T96_d128"])
 def test_golden_fixture(name, gpu_device):
     import os
