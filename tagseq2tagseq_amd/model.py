@@ -167,6 +167,10 @@ class TS2TSModel:
         (to bf16 rounding) to ``forward_inference(tokens, doc_spans)[:, -1:]``."""
         if tokens.shape[0] != 1:
             raise ValueError("the cached path serves one sequence (batch 1)")
+        if self.embedding_weight.dtype != torch.bfloat16:
+            # The key/value cache and the decode kernel are bf16; a float32
+            # model recomputes the sequence on the float32 attention kernels.
+            return self.forward_inference(tokens, doc_spans, **kwargs)[:, -1:]
         # Per-token mask inputs only; the tile tables are built below if the
         # whole sequence has to be recomputed.
         bm = self.block_mask_creator(tokens=tokens, doc_spans=doc_spans or [], inputs_only=True,

@@ -171,6 +171,37 @@ def test_cached_generation_matches_full_recompute(graphs):
     _check_last(m, torch.cat([tok, vocab[:, T:T + 3]], 1), spans2, "new doc")
 
 
+def test_float32_model_inference(monkeypatch):
+    """A model left in float32 (the cache and decode kernel are bf16): the
+    last-row call recomputes on the float32 attention kernels and equals
+    forward_inference's last row; forward_inference itself matches the same
+    model with dense float32 masked attention within 1e-4."""
+    import math
+    import tagseq2tagseq_amd.attention as attn_mod
+    from tests.helpers import dense_mask_torch
+    torch.manual_seed(0)
+    m = TS2TSModel.from_config(vocab_size=500, num_layers=2, model_dim=256, num_heads=4,
+                               max_seq_len=512, dropout=0.0, drop_path_rate=0.0,
+                               block_mask_creator=create_doc_causal_block_mask).to(DEV).eval()
+    g = torch.Generator().manual_seed(2)
+    tokens = torch.randint(0, 500, (1, 300), generator=g).to(DEV)
+    spans = [synth.DocSpan(doc_id=7, start=0, end=120), synth.DocSpan(doc_id=3, start=120, end=300)]
+    full = m.forward_inference(tokens, spans)
+    assert full.dtype == torch.float32
+    assert torch.equal(m.forward_inference_last(tokens, spans), full[:, -1:])
+
+    def dense(q, k, v, block_mask=None, **kw):
+        T = q.shape[2]
+        msk = dense_mask_torch(block_mask.doc_ids[0], None, None, 0, T)
+        sc = (q @ k.transpose(-1, -2)) / math.sqrt(q.shape[-1])
+        return torch.softmax(sc.masked_fill(~msk, float("-inf")), -1).nan_to_num(0.0) @ v
+
+    monkeypatch.setattr(attn_mod, "flex_attention", dense)
+    ref = m.forward_inference(tokens, spans)
+    err = (full - ref).abs().max().item()
+    assert err <= 1e-4 * ref.abs().max().item() + 1e-5, f"float32 logits: max err {err:.3g}"
+
+
 @pytest.mark.parametrize("graphs", [True, False])
 def test_cached_generation_cross_doc_links(graphs):
     m = _model(create_doc_link_block_mask)
