@@ -160,6 +160,25 @@ def test_full_size_against_torch_fp32(cfg, gpu_device):
         assert_close(v.grad[b, hk], ref["dv"][(b, hk)], ATOL, RTOL, f"cfg{cfg} dv b{b} hk{hk}")
 
 
+@pytest.mark.parametrize("seed", range(12))
+def test_fuzz_shapes_and_masks(seed, gpu_device):
+    """Seeded random shapes and masks against the float64 oracle: T from 1 to
+    900 (ragged, below one tile included), batch 1-2 with per-row masks, GQA
+    ratios 1/2/4, D 64/128, 0-3 grant words (bit 63 included), uncovered
+    tokens, bf16 and float32 (at their bounds), forward and backward."""
+    rng = np.random.default_rng(1000 + seed)
+    T = int(rng.choice([1, 2, 31, 127, 128, 129]) if seed < 3 else rng.integers(130, 900))
+    B = int(rng.integers(1, 3))
+    Hkv = int(rng.integers(1, 3))
+    Hq = Hkv * int(rng.choice([1, 2, 4]))
+    D = int(rng.choice([64, 128]))
+    words = int(rng.integers(0, 4))
+    rows = [random_row(T, rng, words=words, uncovered=bool(rng.random() < 0.5),
+                       max_doc=int(rng.integers(8, 300))) for _ in range(B)]
+    dtype = torch.float32 if seed % 3 == 2 else torch.bfloat16
+    _oracle_check(rows, B, Hq, Hkv, T, D, seed=seed, device=gpu_device, dtype=dtype)
+
+
 def test_max_size_T65536(gpu_device):
     """The largest shape exercised: T = 65536 (512 tiles per side, 376
     documents, 6 grant words, ~1 GB of tile-bitmap slots) with the config-4
