@@ -205,7 +205,7 @@ def schedule_bench(args, dev):
     q, k, v, do = (torch.randn(1, H, T, D, generator=g).to(torch.bfloat16).to(dev)
                    for _ in range(4))
     scale = 1.0 / math.sqrt(D)
-    pairs, ms = [], []
+    pairs, ms, tiles = [], [], []
     for s in range(16):
         row = synth.linked_lognormal_docs(T, 350.0, 1.0, 2048, 0.15, seed=100 + s)
         rows_np = [per_token_arrays(row)]
@@ -220,10 +220,18 @@ def schedule_bench(args, dev):
 
         ms.append(time_launches(step, max(3, args.reps // 4)))
         pairs.append(pack_pairs(T, row.spans, row.link_rows))
+        tc = bm.tile_class
+        tiles.append((int((tc == 2).sum()), int((tc == 1).sum())))
     x, y = np.array(pairs, dtype=np.float64), np.array(ms)
     A = np.stack([x, np.ones_like(x)], 1)
     coef, *_ = np.linalg.lstsq(A, y, rcond=None)
     r2 = 1.0 - ((y - A @ coef) ** 2).sum() / ((y - y.mean()) ** 2).sum()
+    # tile-class model (masks given only as per-token grant words): time =
+    # a full + b partial + c; b / a is the partial-tile weight of tile_cost
+    tf = np.array(tiles, dtype=np.float64)
+    At = np.stack([tf[:, 0], tf[:, 1], np.ones(len(tf))], 1)
+    ct, *_ = np.linalg.lstsq(At, y, rcond=None)
+    r2t = 1.0 - ((y - At @ ct) ** 2).sum() / ((y - y.mean()) ** 2).sum()
     # 8 ranks x 64 steps of independent packs, costs from the fitted model
     ranks, steps, window = 8, 64, 16
     raw, ordered = [], []
@@ -245,6 +253,10 @@ def schedule_bench(args, dev):
         "cost_model": {"packs_timed": len(ms), "ms_per_mpair": round(coef[0] * 1e6, 5),
                        "ms_fixed": round(coef[1], 4), "r2": round(float(r2), 4),
                        "ms_range": [round(float(y.min()), 4), round(float(y.max()), 4)]},
+        "tile_cost_model": {"ms_per_full_tile": round(float(ct[0]), 6),
+                            "ms_per_partial_tile": round(float(ct[1]), 6),
+                            "partial_weight": round(float(ct[1] / ct[0]), 3) if ct[0] else None,
+                            "r2": round(float(r2t), 4)},
     }))
 
 

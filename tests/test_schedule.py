@@ -14,7 +14,7 @@ import torch.multiprocessing as mp
 from oracle import mask_oracle as mo
 from tagseq2tagseq_amd import synth
 from tagseq2tagseq_amd.schedule import (DensityOrderedBatches, gather_costs, pack_pairs,
-                                        straggler_fraction)
+                                        straggler_fraction, tile_cost)
 
 
 def _doc_link_bits(T, spans, links):
@@ -143,3 +143,13 @@ def test_two_rank_gloo():
         assert got == want  # each rank keeps exactly its own packs
         assert f_ord <= f_raw
     assert res[0][3] == res[1][3] and res[0][4] == res[1][4]  # same gathered view
+
+
+def test_tile_cost_counts_full_and_weighted_partial_tiles():
+    """tile_cost = full + w * partial over every mask row (skip tiles free)."""
+    import types
+    tc = torch.tensor([[[2, 1, 0], [1, 1, 2], [0, 0, 1]]], dtype=torch.int8)  # 2 full, 4 partial
+    bm = types.SimpleNamespace(tile_class=tc)
+    assert tile_cost(bm, partial_weight=1.0) == 6.0
+    assert tile_cost(bm, partial_weight=0.5) == 4.0
+    assert abs(tile_cost(bm) - (2 + 0.63 * 4)) < 1e-12
