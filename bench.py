@@ -317,6 +317,29 @@ def decode_bench(args, dev):
         model.forward_inference_last(tok, sp, doc_links=links).argmax().item()
     eager_ms = 1e3 * (time.perf_counter() - t0) / n_steps
     model.use_graphs = True
+
+    def replay_us(reps=50):
+        # GPU time of one captured step (the graph alone, no host work)
+        g = model._graph.graph
+        g.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        return 1e3 * e0.elapsed_time(e1) / reps
+
+    step_us = replay_us()
+    # the same steps with the unfused layer sequence (torch GEMMs and
+    # elementwise kernels around the prologue and decode kernels)
+    model.fuse_rows = False
+    for i in range(args.warmup + 1, args.warmup + 1 + n_steps):
+        tok, sp = grown(i)
+        model.forward_inference_last(tok, sp, doc_links=links).argmax().item()
+    unfused_step_us = replay_us()
+    model.fuse_rows = True
     tok, sp = grown(args.warmup + n_steps)
     ref = model.forward_inference(tok, sp, doc_links=links)[:, -1:].float()
     err = (logits.float() - ref).abs().max().item() / ref.abs().max().item()
@@ -386,6 +409,8 @@ def decode_bench(args, dev):
         "data": "synthetic (random token ids, seeded packed documents, random-init weights)",
         "config": {"workload": "decode steps on the configs[4] model", "context": T0,
                    "vocab": V, "n_docs": len(spans), "grant_words": W},
+        "graph_step_gpu_us": round(step_us, 1),
+        "graph_step_gpu_us_unfused_layers": round(unfused_step_us, 1),
         "eager_cached_ms_per_token": round(eager_ms, 3),
         "full_recompute_ms_per_token": round(full_ms, 2),
         "speedup_vs_full_recompute": round(full_ms / cached_ms, 1),

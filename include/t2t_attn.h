@@ -286,6 +286,56 @@ int t2t_rms_norm_backward(const void *dy, int64_t dy_stride, const void *x, int6
                           int64_t dx_stride, void *dweight, void *workspace,
                           int64_t workspace_bytes, int32_t N, int32_t C, void *stream);
 
+/* Epilogues of t2t_rows_linear. */
+#define T2T_ROWS_STORE 0  /* y = W xin */
+#define T2T_ROWS_ADD 1    /* y = res + bf16(W xin) */
+#define T2T_ROWS_SWIGLU 2 /* y = bf16(silu(g)) u, g = W[0:N] xin, u = W[N:2N] xin */
+
+/*
+ * Linear map of a few token rows for a generation step, with the work around
+ * it fused in.  Replaces, at M <= 8 rows, the nn.Linear products of a layer
+ * (model/modules/layer.py:32-35: tunalab FlexSelfAttention's out-projection,
+ * GLU's gate_up and down, and the head's lm_head at model/model.py:227-237)
+ * together with the RMSNorm before them and the residual add or SwiGLU after.
+ *   x        bf16 rows [M][K] (row stride x_stride, elements); K % 8 == 0,
+ *            K <= 4096, 0 <= M <= 8; 16-byte aligned.
+ *   weight   bf16 [N][K] row-major (nn.Linear layout); [2N][K] for SWIGLU
+ *            (gate rows, then up rows: the gate_up output chunked in two).
+ *   norm_weight  optional RMSNorm weight [K] (norm_dtype 0 bf16, 1 float32):
+ *            xin = bf16(x / sqrt(mean(x^2) + eps) * norm_weight), as
+ *            t2t_rms_norm writes it; NULL: xin = x.
+ *   res, y   bf16 rows [M][N]; y may be res (in place), nothing else may alias.
+ * Products are summed in fp32 and rounded to bf16 before the epilogue.
+ */
+int t2t_rows_linear(const void *x, int64_t x_stride, int32_t M, int32_t K, const void *weight,
+                    int32_t N, const void *norm_weight, int32_t norm_dtype, float eps,
+                    int32_t epilogue, const void *res, int64_t res_stride, void *y,
+                    int64_t y_stride, void *stream);
+
+/*
+ * qkv projection of a few rows with the rotary embedding and the key/value
+ * cache write: replaces, in a generation step, the attention module's qkv
+ * nn.Linear, its head split and rotation (t2t_qkv_rope) and the writes of the
+ * new k and v rows into the cache, with the layer's RMSNorm before them
+ * (model/modules/layer.py:33).
+ *   x, norm_weight, eps   as for t2t_rows_linear (K = model dim).
+ *   weight   bf16 [3 H D][K] (q, k, v head blocks, nn.Linear(C, 3C) layout).
+ *   cos, sin float [table_rows][D/2]; row m uses position p = pos[m] (device
+ *            int64[M]) or pos0 + m when pos is NULL.
+ *   q        [H][M][D] view (t axis = row; the b stride is unused) of the
+ *            rotated query rows.
+ *   k_cache, v_cache  [H][cache_rows][D] views: row m's rotated k and plain v
+ *            go to slot p.  A row whose p lies outside
+ *            [0, min(table_rows, cache_rows)) writes nothing (q included).
+ * Rotation as t2t_qkv_rope, on the bf16-rounded products.
+ */
+int t2t_rows_qkv_rope(const void *x, int64_t x_stride, int32_t M, int32_t K, const void *weight,
+                      const void *norm_weight, int32_t norm_dtype, float eps, int32_t H,
+                      int32_t D, const float *cos, const float *sin, int32_t table_rows,
+                      const int64_t *pos, int32_t pos0, const t2t_tensor *q,
+                      const t2t_tensor *k_cache, const t2t_tensor *v_cache, int32_t cache_rows,
+                      void *stream);
+
 #ifdef __cplusplus
 }
 #endif

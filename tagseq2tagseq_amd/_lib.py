@@ -17,6 +17,8 @@ HEADER_PATH = os.path.join(os.path.dirname(HERE), "include", "t2t_attn.h")
 T2T_OK = 0
 T2T_DTYPE_BF16 = 0
 T2T_DTYPE_F32 = 1
+T2T_ROWS_STORE, T2T_ROWS_ADD, T2T_ROWS_SWIGLU = 0, 1, 2
+ROWS_MAX = 8
 TILE = 128
 MAX_WORDS = 8
 TILE_BITS_WORDS = 1024  # uint32 per tile bitmap slot ([2][128][4])
@@ -63,6 +65,10 @@ _SIGS = {
                                _I32, _P], ctypes.c_int),
     "t2t_attn_decode": ([_P] * 7 + [_I64] + [_P] * 3 + [_I32] * 9 + [ctypes.c_float, _P, _I64, _P],
                         ctypes.c_int),
+    "t2t_rows_linear": ([_P, _I64, _I32, _I32, _P, _I32, _P, _I32, ctypes.c_float, _I32, _P, _I64,
+                         _P, _I64, _P], ctypes.c_int),
+    "t2t_rows_qkv_rope": ([_P, _I64, _I32, _I32, _P, _P, _I32, ctypes.c_float, _I32, _I32, _P, _P,
+                           _I32, _P, _I32, _P, _P, _P, _I32, _P], ctypes.c_int),
 }
 
 

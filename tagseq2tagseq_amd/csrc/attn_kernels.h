@@ -126,4 +126,21 @@ hipError_t launch_rmsnorm_bwd(const __bf16* dy, int64_t dys, const __bf16* x, in
                               int64_t dxs, void* dw, float* part, int N, int C,
                               hipStream_t stream);
 
+// Linear maps of M <= 8 token rows (K % 8 == 0, K <= 4096) with an optional
+// RMSNorm of the input and a fused epilogue; the modes match T2T_ROWS_*.
+enum RowsMode { kRowsStore = 0, kRowsAdd = 1, kRowsSwiglu = 2, kRowsQkvRope = 3 };
+constexpr int kRowsMaxRows = 8;
+hipError_t launch_rows_linear(int mode, const __bf16* x, int64_t xs, int M, int K,
+                              const __bf16* w, int N, const void* norm_w, bool norm_f32,
+                              float eps, const __bf16* res, int64_t rs, __bf16* y, int64_t ys,
+                              hipStream_t stream);
+// qkv projection of the rows, rotated q rows to q [H][M][D] and rotated k /
+// plain v rows to the cache views at the rows' positions (pos[m], or
+// pos0 + m when pos is NULL); positions outside [0, max_pos) are not written.
+hipError_t launch_rows_qkv_rope(const __bf16* x, int64_t xs, int M, int K, const __bf16* w,
+                                const void* norm_w, bool norm_f32, float eps, int H, int D,
+                                const float* cos, const float* sin, const int64_t* pos, int pos0,
+                                int max_pos, const TensorView& q, const TensorView& k,
+                                const TensorView& v, hipStream_t stream);
+
 }  // namespace t2t

@@ -1,5 +1,6 @@
 // extern "C" boundary of libt2t_attn.so: argument validation, error
 // reporting and dispatch to the gfx950 kernels.  No allocation happens here.
+#include <algorithm>
 #include <cstdarg>
 #include <cstdio>
 
@@ -445,6 +446,86 @@ int t2t_rms_norm_backward(const void* dy, int64_t dy_stride, const void* x, int6
                               static_cast<float*>(workspace), N, C,
                               static_cast<hipStream_t>(stream)),
       "t2t_rms_norm_backward launch");
+}
+
+}  // extern "C"
+
+namespace {
+
+int check_rows(int M, int K, int N, const void* x, int64_t x_stride, const void* weight,
+               const void* norm_weight, int norm_dtype) {
+  if (M < 0 || M > t2t::kRowsMaxRows)
+    return fail(T2T_EUNSUPPORTED, "M = %d rows; 0 to %d supported", M, t2t::kRowsMaxRows);
+  if (K < 8 || K > 4096 || K % 8)
+    return fail(T2T_EUNSUPPORTED, "K = %d is not a multiple of 8 in [8, 4096]", K);
+  if (N < 1) return fail(T2T_EINVAL, "N = %d", N);
+  if (!x || !weight) return fail(T2T_EINVAL, "x or weight is NULL");
+  if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(weight)) % 16)
+    return fail(T2T_EINVAL, "x and weight must be 16-byte aligned");
+  if (x_stride < K || x_stride % 8)
+    return fail(T2T_EINVAL, "x row stride %lld is below K or not a multiple of 8",
+                (long long)x_stride);
+  if (norm_weight) {
+    if (norm_dtype != 0 && norm_dtype != 1)
+      return fail(T2T_EUNSUPPORTED, "norm weight dtype %d (0 bf16, 1 f32)", norm_dtype);
+    if (reinterpret_cast<uintptr_t>(norm_weight) % 16)
+      return fail(T2T_EINVAL, "norm weight must be 16-byte aligned");
+  }
+  return T2T_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int t2t_rows_linear(const void* x, int64_t x_stride, int32_t M, int32_t K, const void* weight,
+                    int32_t N, const void* norm_weight, int32_t norm_dtype, float eps,
+                    int32_t epilogue, const void* res, int64_t res_stride, void* y,
+                    int64_t y_stride, void* stream) {
+  int rc = check_rows(M, K, N, x, x_stride, weight, norm_weight, norm_dtype);
+  if (rc) return rc;
+  if (epilogue != T2T_ROWS_STORE && epilogue != T2T_ROWS_ADD && epilogue != T2T_ROWS_SWIGLU)
+    return fail(T2T_EUNSUPPORTED, "epilogue %d (0 store, 1 add, 2 swiglu)", epilogue);
+  if (!y) return fail(T2T_EINVAL, "y is NULL");
+  if (y_stride < N) return fail(T2T_EINVAL, "y row stride %lld is below N", (long long)y_stride);
+  if (epilogue == T2T_ROWS_ADD && (!res || res_stride < N))
+    return fail(T2T_EINVAL, "the add epilogue needs res with a row stride of at least N");
+  if (M == 0) return T2T_OK;
+  return hip_status(
+      t2t::launch_rows_linear(epilogue, static_cast<const __bf16*>(x), x_stride, M, K,
+                              static_cast<const __bf16*>(weight), N, norm_weight, norm_dtype == 1,
+                              eps, static_cast<const __bf16*>(res), res_stride,
+                              static_cast<__bf16*>(y), y_stride, static_cast<hipStream_t>(stream)),
+      "t2t_rows_linear launch");
+}
+
+int t2t_rows_qkv_rope(const void* x, int64_t x_stride, int32_t M, int32_t K, const void* weight,
+                      const void* norm_weight, int32_t norm_dtype, float eps, int32_t H,
+                      int32_t D, const float* cos, const float* sin, int32_t table_rows,
+                      const int64_t* pos, int32_t pos0, const t2t_tensor* q,
+                      const t2t_tensor* k_cache, const t2t_tensor* v_cache, int32_t cache_rows,
+                      void* stream) {
+  if (H < 1 || D < 2 || D % 2 || (int64_t)H * D > (1 << 20))
+    return fail(T2T_EUNSUPPORTED, "H = %d, D = %d (H >= 1, even D)", H, D);
+  int rc = check_rows(M, K, H * D, x, x_stride, weight, norm_weight, norm_dtype);
+  if (rc) return rc;
+  if (!cos || !sin) return fail(T2T_EINVAL, "cos or sin is NULL");
+  if (table_rows < 0 || cache_rows < 0 || pos0 < 0)
+    return fail(T2T_EINVAL, "negative table_rows, cache_rows or pos0");
+  if (!pos && (int64_t)pos0 + M > std::min(table_rows, cache_rows))
+    return fail(T2T_EINVAL, "positions %d..%d exceed the %d table rows or %d cache rows", pos0,
+                pos0 + M - 1, table_rows, cache_rows);
+  for (const t2t_tensor* t : {q, k_cache, v_cache})
+    if (!t || !t->data || t->stride_h < 0 || t->stride_t <= 0)
+      return fail(T2T_EINVAL, "q / k_cache / v_cache view invalid (NULL or bad stride)");
+  if (M == 0) return T2T_OK;
+  return hip_status(
+      t2t::launch_rows_qkv_rope(static_cast<const __bf16*>(x), x_stride, M, K,
+                                static_cast<const __bf16*>(weight), norm_weight, norm_dtype == 1,
+                                eps, H, D, cos, sin, pos, pos0, std::min(table_rows, cache_rows),
+                                as_view(q), as_view(k_cache), as_view(v_cache),
+                                static_cast<hipStream_t>(stream)),
+      "t2t_rows_qkv_rope launch");
 }
 
 }  // extern "C"

@@ -33,6 +33,7 @@ from .block_mask import T2TBlockMask, build_block_mask
 from .decode import MAX_ROWS, attn_decode
 from .modules import RMSNorm, TS2TSBackbone
 from .rope import qkv_rope
+from .rows import applies as rows_apply, rows_linear, rows_qkv_rope
 
 
 class KVCache:
@@ -95,6 +96,7 @@ class TS2TSModel:
         self.kv_cache: Optional[KVCache] = None
         self.prefill_rows = 64
         self.use_graphs = True
+        self.fuse_rows = True  # few-row steps on the fused row kernels (rows.py)
         self._graph: Optional[_DecodeGraph] = None
 
     @classmethod
@@ -195,12 +197,15 @@ class TS2TSModel:
         x = F.embedding(tokens[:, p0:], self.embedding_weight)
         x = self._backbone_rows(x, bm, cache, p0, full)
         cache.length = T
-        x = self.norm(x[:, -1:])
-        return F.linear(x, self.lm_head_weight)
+        x = x[:, -1:]
+        if self._rows_fusable(x):
+            return rows_linear(x, self.lm_head_weight, norm=self.norm)
+        return F.linear(self.norm(x), self.lm_head_weight)
 
     def _graph_step(self, cache: KVCache, tokens: torch.Tensor, bm, p: int) -> torch.Tensor:
         """One new row at position p through the captured decode step."""
-        if self._graph is None or self._graph.cache is not cache:
+        if (self._graph is None or self._graph.cache is not cache
+                or self._graph.fused != self.fuse_rows):
             self._graph = _DecodeGraph(self, cache)
         return self._graph.run(tokens, bm, p)
 
@@ -211,8 +216,10 @@ class TS2TSModel:
         excluded by the causal test), final norm and LM head."""
         x = F.embedding(buf.tok, self.embedding_weight)
         cos_t, sin_t = self._layers()[0].attn.rotary.tables(x.device)
-        cos = cos_t.index_select(0, buf.pos)
-        sin = sin_t.index_select(0, buf.pos)
+        fused = self._rows_fusable(x)
+        if not fused:
+            cos = cos_t.index_select(0, buf.pos)
+            sin = sin_t.index_select(0, buf.pos)
         bb = self.backbone
         skips = []
         n_skip = len(bb.skip_weights)
@@ -221,18 +228,58 @@ class TS2TSModel:
                 x = x + bb.skip_weights[i - n_skip] * skips.pop()
             attn = layer.attn
             C = x.shape[-1]
-            q, k, v = qkv_rope(attn.qkv(layer.ln_1(x)), cos, sin, attn.num_heads, 0)
-            cache.k[i].index_copy_(2, buf.pos, k)
-            cache.v[i].index_copy_(2, buf.pos, v)
+            if fused:
+                q = rows_qkv_rope(x, attn.qkv.weight, attn.num_heads, cos_t, sin_t, buf.pos,
+                                  cache.k[i], cache.v[i], norm=layer.ln_1)
+            else:
+                q, k, v = qkv_rope(attn.qkv(layer.ln_1(x)), cos, sin, attn.num_heads, 0)
+                cache.k[i].index_copy_(2, buf.pos, k)
+                cache.v[i].index_copy_(2, buf.pos, v)
             y, _ = attn_decode(q, cache.k[i], cache.v[i], cache.capacity, cache.doc,
                                cache.kv_bits if cache.words else None, buf.qpos, buf.qdoc,
                                buf.qbits)
-            y = attn.proj(y.transpose(1, 2).reshape(1, 1, C))
-            x = x + layer.drop_path(y)
-            x = x + layer.drop_path(layer.mlp(layer.ln_2(x)))
+            x = self._layer_tail(layer, y.transpose(1, 2).reshape(1, 1, C), x, fused)
             if i < n_skip:
                 skips.append(x)
+        if fused:
+            return rows_linear(x, self.lm_head_weight, norm=self.norm)
         return F.linear(self.norm(x), self.lm_head_weight)
+
+    def _rows_fusable(self, x) -> bool:
+        """Whether the layers of a few-row step can run on the fused row
+        kernels (rows.py): bf16 rows and weights on the GPU, at most 8 rows,
+        SwiGLU GLUs, and dropout / drop-path that are the identity."""
+        if (not self.fuse_rows or not rows_apply(x, self.lm_head_weight)
+                or not self.lm_head_weight.is_contiguous()):
+            return False
+        for layer in self._layers():
+            mlp = layer.mlp
+            if (mlp.act is not F.silu or not isinstance(layer.ln_1, RMSNorm)
+                    or not isinstance(layer.ln_2, RMSNorm)):
+                return False
+            if layer.training and (layer.drop_path.p > 0 or mlp.dropout.p > 0):
+                return False
+            ws = (layer.attn.qkv.weight, layer.attn.proj.weight, mlp.gate_up.weight,
+                  mlp.down.weight)
+            if not all(w.dtype == torch.bfloat16 and w.is_contiguous() for w in ws):
+                return False
+            if mlp.down.weight.shape[1] > 4096:
+                return False
+        return isinstance(self.norm, RMSNorm)
+
+    @staticmethod
+    def _layer_tail(layer, y, x, fused: bool):
+        """Out-projection + residual, norm + GLU + residual of Layer.forward
+        (model/modules/layer.py:33-34) on the attention rows y."""
+        if fused:
+            mlp = layer.mlp
+            x = rows_linear(y, layer.attn.proj.weight, epilogue="add", res=x)
+            h = rows_linear(x, mlp.gate_up.weight, norm=layer.ln_2, epilogue="swiglu")
+            if h.shape[-1] % 8:  # rows the kernel cannot read as 16-byte vectors
+                return x + mlp.down(h)
+            return rows_linear(h, mlp.down.weight, epilogue="add", res=x)
+        x = x + layer.drop_path(layer.attn.proj(y))
+        return x + layer.drop_path(layer.mlp(layer.ln_2(x)))
 
     def _backbone_rows(self, x, bm, cache: KVCache, p0: int, full: bool):
         """TS2TSBackbone.forward (skip wiring of model/modules/backbone.py:93-104)
@@ -240,23 +287,29 @@ class TS2TSModel:
         bb = self.backbone
         skips = []
         n_skip = len(bb.skip_weights)
+        fused = not full and self._rows_fusable(x)
         for i, layer in enumerate(bb.layers):
             if i >= n_skip and skips:
                 x = x + bb.skip_weights[i - n_skip] * skips.pop()
-            x = self._layer_rows(i, layer, x, bm, cache, p0, full)
+            x = self._layer_rows(i, layer, x, bm, cache, p0, full, fused)
             if i < n_skip:
                 skips.append(x)
         return x
 
-    def _layer_rows(self, i: int, layer, x, bm, cache: KVCache, p0: int, full: bool):
+    def _layer_rows(self, i: int, layer, x, bm, cache: KVCache, p0: int, full: bool,
+                    fused: bool):
         """Layer.forward (model/modules/layer.py:32-35) over the new rows."""
         attn = layer.attn
         B, n, C = x.shape
         T = p0 + n
         cos, sin = attn.rotary.tables(x.device)
-        q, k, v = qkv_rope(attn.qkv(layer.ln_1(x)), cos, sin, attn.num_heads, p0)
-        cache.k[i, :, :, p0:T] = k
-        cache.v[i, :, :, p0:T] = v
+        if fused:
+            q = rows_qkv_rope(x, attn.qkv.weight, attn.num_heads, cos, sin, p0, cache.k[i],
+                              cache.v[i], norm=layer.ln_1)
+        else:
+            q, k, v = qkv_rope(attn.qkv(layer.ln_1(x)), cos, sin, attn.num_heads, p0)
+            cache.k[i, :, :, p0:T] = k
+            cache.v[i, :, :, p0:T] = v
         if full:
             y = flex_attention(q, k, v, block_mask=bm)
         else:
@@ -270,9 +323,7 @@ class TS2TSModel:
                             cache.kv_bits if bm.words else None, pos[:, c0:c1].contiguous(),
                             bm.doc_ids[:, p0 + c0:p0 + c1].contiguous(), qb,
                             out=y[:, :, c0:c1])
-        y = attn.proj(y.transpose(1, 2).reshape(B, n, C))
-        x = x + layer.drop_path(y)
-        return x + layer.drop_path(layer.mlp(layer.ln_2(x)))
+        return self._layer_tail(layer, y.transpose(1, 2).reshape(B, n, C), x, fused)
 
 
 class _DecodeGraph:
@@ -280,9 +331,10 @@ class _DecodeGraph:
     (torch.cuda.graph) over static buffers: token id, position (int64 for
     index_select / index_copy_, int32 for the decode kernel) and the new
     row's doc id and q words.  Replays cost one launch from the host instead
-    of the ~30 launches per layer of the eager step; the recorded kernels
-    (hipBLASLt GEMMs, torch elementwise / reduction kernels, the prologue and
-    decode kernels) write no memset nodes of their own."""
+    of the launches of the eager step (six per layer on the fused row
+    kernels, ~15 without them); the recorded kernels (the row kernels and
+    the decode kernels, or hipBLASLt GEMMs, torch elementwise / reduction
+    kernels and the prologue kernel) write no memset nodes of their own."""
 
     def __init__(self, model: TS2TSModel, cache: KVCache):
         dev = cache.k.device
@@ -294,6 +346,7 @@ class _DecodeGraph:
         self.qbits = (torch.zeros((1, cache.words, 1), dtype=torch.int64, device=dev)
                       if cache.words else None)
         self.model = model
+        self.fused = model.fuse_rows
         self.graph = None
         self.logits = None
 

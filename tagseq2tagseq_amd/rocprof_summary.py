@@ -46,9 +46,15 @@ def _label(cfg) -> str:
 def _short(name: str) -> str:
     """Kernel name without the namespace / template / argument decoration."""
     base = name.replace("(anonymous namespace)", "").split("(")[0]
+    tmpl = ""
     if "<" in base:
-        base = base.split("<")[0]
-    return base.split("::")[-1].replace("void ", "").strip()
+        base, tmpl = base.split("<", 1)
+    base = base.split("::")[-1].replace("void ", "").strip()
+    if base == "rows_linear_kernel":  # <K chunks per lane, rows, epilogue>: one line per shape
+        mode = ("store", "add", "swiglu", "qkv_rope")[int(tmpl.rstrip(">").split(",")[-1])]
+        kv, mt = (int(t) for t in tmpl.split(",")[:2])
+        return f"rows_linear[K<={512 * kv},M<={mt},{mode}]"
+    return base
 
 
 def _db(path: str) -> sqlite3.Connection:
@@ -108,12 +114,12 @@ def trace(kt_dir: str, bench_json: str, cfg: str, bench_args: str = "") -> str:
         "# mean per call from the JSON line of the same profiled run (token_inputs: the whole",
         "# TokenLists.build() call, host side included).",
         "",
-        f"{'kernel':28s} {'calls':>6s} {'mean':>8s} {'median':>8s} {'min':>8s} {'max':>8s}   bench.py HIP events",
+        f"{'kernel':36s} {'calls':>6s} {'mean':>8s} {'median':>8s} {'min':>8s} {'max':>8s}   bench.py HIP events",
     ]
     for k, v in sorted(durs.items(), key=lambda kv: -statistics.mean(kv[1])):
         evk = next((ev[e] for e in ev if e.startswith(k)), None)
         evs = f"{1000 * evk:10.1f}" if evk is not None else "         -"
-        lines.append(f"{k:28s} {len(v):6d} {statistics.mean(v):8.1f} {statistics.median(v):8.1f} "
+        lines.append(f"{k:36s} {len(v):6d} {statistics.mean(v):8.1f} {statistics.median(v):8.1f} "
                      f"{min(v):8.1f} {max(v):8.1f}   {evs}")
     lines.append("")
     lines.append(f"# bench.py line of that run: value {bench.get('value')} {bench.get('unit')}, "

@@ -120,8 +120,10 @@ def test_too_many_rows_raises():
 # -- cached model path ------------------------------------------------------
 
 def _model(creator, T_max=1024):
+    # model_dim 384: GLU hidden width 1024, a multiple of 8, so few-row steps
+    # run on the fused row kernels
     torch.manual_seed(0)
-    m = TS2TSModel.from_config(vocab_size=500, num_layers=4, model_dim=256, num_heads=4,
+    m = TS2TSModel.from_config(vocab_size=500, num_layers=4, model_dim=384, num_heads=6,
                                max_seq_len=T_max, dropout=0.0, drop_path_rate=0.0,
                                block_mask_creator=creator)
     with torch.no_grad():
@@ -222,3 +224,45 @@ def test_cached_generation_cross_doc_links(graphs):
     links2 = links.copy()
     links2[3, 0] |= np.uint64(1)  # the generated doc gains a link: its rows change
     _check_last(m, vocab[:, :T], spans, "link added", doc_links=links2)
+
+
+@pytest.mark.parametrize("graphs", [True, False])
+@pytest.mark.parametrize("dim,heads", [(384, 6), (256, 4)])
+def test_fused_row_kernels_match_unfused_layers(graphs, dim, heads, monkeypatch):
+    """Decode steps on the fused row kernels (norm + qkv + rotation + cache
+    write, out-projection + residual, norm + gate_up + SwiGLU, down +
+    residual, norm + LM head) against the same steps through the unfused torch
+    layer sequence, one and five rows at a time.  dim 256 has a GLU hidden
+    width of 682, not a multiple of 8: its down-projection stays a torch
+    product, the rest is fused."""
+    import tagseq2tagseq_amd.model as model_mod
+    calls = []
+    real = model_mod.rows_linear
+    monkeypatch.setattr(model_mod, "rows_linear",
+                        lambda *a, **kw: calls.append(1) or real(*a, **kw))
+    torch.manual_seed(0)
+    m = TS2TSModel.from_config(vocab_size=500, num_layers=4, model_dim=dim, num_heads=heads,
+                               max_seq_len=1024, dropout=0.0, drop_path_rate=0.0,
+                               block_mask_creator=create_doc_causal_block_mask)
+    with torch.no_grad():
+        m.embedding_weight.mul_(0.05)
+    m = m.to(DEV, torch.bfloat16).eval()
+    m.use_graphs = graphs
+    g = torch.Generator().manual_seed(3)
+    vocab = torch.randint(0, 500, (1, 1024), generator=g).to(DEV)
+    spans = [synth.DocSpan(doc_id=1, start=0, end=200)]
+    T = 200
+    m.forward_inference_last(vocab[:, :T], spans)
+    for n in (1, 1, 5, 1):
+        spans = _grow(spans, n)
+        T += n
+        m.fuse_rows = True
+        fused = m.forward_inference_last(vocab[:, :T], spans).float()
+        m.fuse_rows = False
+        m.kv_cache.length = T - n  # recompute the same rows unfused
+        m.kv_cache.tokens[0, T - n:T] = -1
+        plain = m.forward_inference_last(vocab[:, :T], spans).float()
+        scale = plain.abs().max().item()
+        err = (fused - plain).abs().max().item()
+        assert err <= 2e-2 * scale + 1e-3, f"{n} rows: max err {err:.4g} (scale {scale:.3g})"
+    assert calls, "the fused row kernels did not run"

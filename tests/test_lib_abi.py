@@ -212,3 +212,45 @@ def test_attn_decode_argument_checks():
     assert call(words=1) == -1 and "NULL" in _err()
     assert call(ws_bytes=ws - 4) == -1 and "workspace" in _err()
     assert call(words=9) == -2
+
+
+def test_rows_linear_argument_checks():
+    """t2t_rows_linear / t2t_rows_qkv_rope reject bad shapes and pointers
+    before any launch (no GPU needed)."""
+    lib = _lib.lib()
+    P = ctypes.c_void_p(0x1000)
+
+    def lin(M=1, K=768, N=768, x=P, xs=768, w=P, nw=None, ndt=0, ep=0, res=None, rs=0, y=P,
+            ys=768):
+        return lib.t2t_rows_linear(x, xs, M, K, w, N, nw, ndt, 1e-6, ep, res, rs, y, ys, None)
+
+    assert lin(M=9) == -2 and "rows" in _err()
+    assert lin(M=-1) == -2
+    assert lin(K=12, xs=16) == -2 and "multiple of 8" in _err()
+    assert lin(K=4104, xs=4104) == -2
+    assert lin(N=0) == -1
+    assert lin(x=None) == -1 and "NULL" in _err()
+    assert lin(x=ctypes.c_void_p(0x1008)) == -1 and "aligned" in _err()
+    assert lin(xs=760) == -1 and "stride" in _err()
+    assert lin(nw=P, ndt=2) == -2 and "dtype" in _err()
+    assert lin(ep=3) == -2 and "epilogue" in _err()
+    assert lin(y=None) == -1
+    assert lin(ys=700) == -1 and "stride" in _err()
+    assert lin(ep=1) == -1 and "res" in _err()
+    assert lin(ep=1, res=P, rs=100) == -1
+    assert lin(M=0) == 0  # nothing to do, nothing launched
+
+    v = _dummy_view()
+
+    def qkv(M=1, K=768, H=12, D=64, pos=None, pos0=0, rows=128, cache=128, views=(v, v, v)):
+        return lib.t2t_rows_qkv_rope(P, K, M, K, P, None, 0, 1e-6, H, D, P, P, rows, pos, pos0,
+                                     *[ctypes.byref(t) for t in views], cache, None)
+
+    assert qkv(D=63) == -2
+    assert qkv(H=0) == -2
+    assert qkv(M=9) == -2
+    assert qkv(pos0=127, M=2) == -1 and "exceed" in _err()
+    assert qkv(pos0=126, M=2, cache=127) == -1 and "cache rows" in _err()
+    bad = _lib.T2TTensor(0, 0, 0, 64)
+    assert qkv(views=(v, bad, v)) == -1 and "view" in _err()
+    assert qkv(M=0) == 0
