@@ -23,7 +23,9 @@
 // dot products are summed across them with DPP butterflies.  Pass 1 writes the
 // chunk's scores to LDS, pass 2 takes the chunk's row max, weights the V rows
 // by exp2(s - max) and sums them across the key groups (DPP, then LDS across
-// waves).  Each (row, chunk) leaves (max, sum, unnormalised o[D]) in the
+// waves).  The kernel has two dependent memory stages: the keys' mask
+// inputs with the query rows, then the K and V rows of the allowed keys.
+// Each (row, chunk) leaves (max, sum, unnormalised o[D]) in the
 // workspace; attn_decode_combine merges the chunks of a row into o (bf16)
 // and the log2-domain LSE.  Fully masked rows give o = 0 and LSE = -inf.
 #include "attn_kernels.h"
@@ -83,6 +85,22 @@ __global__ __launch_bounds__(kDecThreads) void attn_decode_partial(DecodeArgs a)
   const int mb = a.Bm > 1 ? b : 0;
   const int j0 = chunk * kDecChunk;
 
+  const __bf16* kbase = static_cast<const __bf16*>(a.k.data) + b * a.k.sb + hk * a.k.sh + 8 * dg;
+  const __bf16* vbase = static_cast<const __bf16*>(a.v.data) + b * a.v.sb + hk * a.v.sh + 8 * dg;
+  const int32_t* kdoc = a.key_doc + (size_t)mb * a.key_stride;
+  const uint64_t* kbits = a.key_bits + (size_t)mb * a.W * a.key_stride;
+
+  // The keys' doc ids and first grant word depend on nothing else: their
+  // loads go out first, with the query rows' and the new rows' mask inputs.
+  int dj[KPG];
+  uint64_t kw0[KPG];
+#pragma unroll
+  for (int i = 0; i < KPG; ++i) {
+    const int j = j0 + kg + NKG * i;
+    dj[i] = j < a.Tkv ? kdoc[j] : 0;
+    kw0[i] = (a.W > 0 && j < a.Tkv) ? kbits[j] : 0ull;
+  }
+
   if (tid < a.Tq) {
     qpos_s[tid] = a.q_pos[(size_t)mb * a.Tq + tid];
     qdoc_s[tid] = a.q_doc[(size_t)mb * a.Tq + tid];
@@ -108,23 +126,13 @@ __global__ __launch_bounds__(kDecThreads) void attn_decode_partial(DecodeArgs a)
   }
   __syncthreads();
 
-  const __bf16* kbase = static_cast<const __bf16*>(a.k.data) + b * a.k.sb + hk * a.k.sh + 8 * dg;
-  const __bf16* vbase = static_cast<const __bf16*>(a.v.data) + b * a.v.sb + hk * a.v.sh + 8 * dg;
-  const int32_t* kdoc = a.key_doc + (size_t)mb * a.key_stride;
-  const uint64_t* kbits = a.key_bits + (size_t)mb * a.W * a.key_stride;
-
   // Mask of the group's keys j0 + kg + NKG i: bit tq of allow[i] = allowed for
   // new row tq.  Every load of a stage is issued before any is consumed, so a
   // stage costs one memory latency, not one per key.
   uint32_t allow[KPG];
   {
-    int dj[KPG];
 #pragma unroll
-    for (int i = 0; i < KPG; ++i) {
-      const int j = j0 + kg + NKG * i;
-      dj[i] = j < a.Tkv ? kdoc[j] : 0;
-      allow[i] = 0;
-    }
+    for (int i = 0; i < KPG; ++i) allow[i] = 0;
     for (int tq = 0; tq < a.Tq; ++tq) {
       const int qd = qdoc_s[tq];
 #pragma unroll
@@ -135,7 +143,7 @@ __global__ __launch_bounds__(kDecThreads) void attn_decode_partial(DecodeArgs a)
 #pragma unroll
       for (int i = 0; i < KPG; ++i) {
         const int j = j0 + kg + NKG * i;
-        kw[i] = j < a.Tkv ? kbits[(size_t)w * a.key_stride + j] : 0ull;
+        kw[i] = w == 0 ? kw0[i] : (j < a.Tkv ? kbits[(size_t)w * a.key_stride + j] : 0ull);
       }
       for (int tq = 0; tq < a.Tq; ++tq) {
         const uint64_t qw = qbits_s[w][tq];
@@ -152,14 +160,19 @@ __global__ __launch_bounds__(kDecThreads) void attn_decode_partial(DecodeArgs a)
     }
   }
 
-  // Pass 1: K rows of the allowed keys, scores to LDS (-inf where masked).
+  // Pass 1: K and V rows of the allowed keys (both issued here: V depends
+  // only on the mask), scores to LDS (-inf where masked).
+  bf16x8 vx[KPG];
   {
     bf16x8 kx[KPG];
 #pragma unroll
     for (int i = 0; i < KPG; ++i) {
       kx[i] = bf16x8{};
-      if (allow[i])
+      vx[i] = bf16x8{};
+      if (allow[i]) {
         kx[i] = *reinterpret_cast<const bf16x8*>(kbase + (int64_t)(j0 + kg + NKG * i) * a.k.st);
+        vx[i] = *reinterpret_cast<const bf16x8*>(vbase + (int64_t)(j0 + kg + NKG * i) * a.v.st);
+      }
     }
 #pragma unroll
     for (int i = 0; i < KPG; ++i) {
@@ -198,13 +211,6 @@ __global__ __launch_bounds__(kDecThreads) void attn_decode_partial(DecodeArgs a)
     for (int e = 0; e < 8; ++e) o[r][e] = 0.f;
   }
   {
-    bf16x8 vx[KPG];
-#pragma unroll
-    for (int i = 0; i < KPG; ++i) {
-      vx[i] = bf16x8{};
-      if (allow[i])
-        vx[i] = *reinterpret_cast<const bf16x8*>(vbase + (int64_t)(j0 + kg + NKG * i) * a.v.st);
-    }
 #pragma unroll
     for (int i = 0; i < KPG; ++i) {
       const int jl = kg + NKG * i;

@@ -67,6 +67,15 @@ class KVCache:
         idx = torch.nonzero(diff)
         return int(idx[0, 0]) if idx.numel() else n
 
+    def prefix_changed(self, tokens: torch.Tensor, bm, n: int) -> torch.Tensor:
+        """Device bool: whether the token id or a mask input of any of the
+        first n positions differs from the cached ones (no host sync)."""
+        d = (self.tokens[0, :n] != tokens[0, :n]).any() | (self.doc[0, :n] != bm.doc_ids[0, :n]).any()
+        if self.words:
+            d |= (self.q_bits[0, :, :n] != bm.q_bits[0, :, :n]).any()
+            d |= (self.kv_bits[0, :, :n] != bm.kv_bits[0, :, :n]).any()
+        return d
+
     def store_inputs(self, tokens: torch.Tensor, bm, p0: int, p1: int) -> None:
         self.tokens[0, p0:p1] = tokens[0, p0:p1]
         self.doc[0, p0:p1] = bm.doc_ids[0, p0:p1]
@@ -182,6 +191,20 @@ class TS2TSModel:
         if cache is None or cache.words != bm.words or T > cache.capacity:
             cache = self.kv_cache = self._new_cache(bm.words, tokens.device)
             self._graph = None
+        p = T - 1
+        if self.use_graphs and p >= 1 and cache.length >= p:
+            # The generation case: the cached prefix covers every position but
+            # the last.  Launch the single-row step at once and check the
+            # prefix on the device beside it; the check is read back after the
+            # step's launches, so the step costs one host synchronisation.
+            cache.store_inputs(tokens, bm, p, T)
+            logits = self._graph_step(cache, tokens, bm, p)
+            changed = cache.prefix_changed(tokens, bm, p)  # reads positions < p only
+            if not bool(changed):
+                cache.length = T
+                return logits
+            # an earlier input changed: recompute from the first difference
+            cache.length = p
         p0 = min(cache.reusable_prefix(tokens, bm), T - 1)
         full = T - p0 > self.prefill_rows
         if full:
@@ -207,14 +230,20 @@ class TS2TSModel:
         if (self._graph is None or self._graph.cache is not cache
                 or self._graph.fused != self.fuse_rows):
             self._graph = _DecodeGraph(self, cache)
-        return self._graph.run(tokens, bm, p)
+        return self._graph.run(p)
 
     def _step_body(self, cache: KVCache, buf: "_DecodeGraph") -> torch.Tensor:
         """The single-row step over static buffers (no host values in any
         launch): embedding, every layer with its cache write and decode
         attention over the whole cache capacity (slots past the new row are
         excluded by the causal test), final norm and LM head."""
-        x = F.embedding(buf.tok, self.embedding_weight)
+        # The new row's token id and mask inputs, written into the cache at
+        # position pos before every replay, are gathered inside the graph.
+        tok = cache.tokens.index_select(1, buf.pos)
+        qdoc = cache.doc.index_select(1, buf.pos)
+        qbits = cache.q_bits.index_select(2, buf.pos) if cache.words else None
+        qpos = buf.pos.to(torch.int32).view(1, 1)
+        x = F.embedding(tok, self.embedding_weight)
         cos_t, sin_t = self._layers()[0].attn.rotary.tables(x.device)
         fused = self._rows_fusable(x)
         if not fused:
@@ -236,8 +265,7 @@ class TS2TSModel:
                 cache.k[i].index_copy_(2, buf.pos, k)
                 cache.v[i].index_copy_(2, buf.pos, v)
             y, _ = attn_decode(q, cache.k[i], cache.v[i], cache.capacity, cache.doc,
-                               cache.kv_bits if cache.words else None, buf.qpos, buf.qdoc,
-                               buf.qbits)
+                               cache.kv_bits if cache.words else None, qpos, qdoc, qbits)
             x = self._layer_tail(layer, y.transpose(1, 2).reshape(1, 1, C), x, fused)
             if i < n_skip:
                 skips.append(x)
@@ -328,23 +356,18 @@ class TS2TSModel:
 
 class _DecodeGraph:
     """The single-row decode step of a TS2TSModel captured as a HIP graph
-    (torch.cuda.graph) over static buffers: token id, position (int64 for
-    index_select / index_copy_, int32 for the decode kernel) and the new
-    row's doc id and q words.  Replays cost one launch from the host instead
-    of the launches of the eager step (six per layer on the fused row
-    kernels, ~15 without them); the recorded kernels (the row kernels and
-    the decode kernels, or hipBLASLt GEMMs, torch elementwise / reduction
-    kernels and the prologue kernel) write no memset nodes of their own."""
+    (torch.cuda.graph) over one static buffer, the row's position: the step
+    gathers the row's token id and mask inputs from the cache, where
+    ``store_inputs`` has written them before the replay.  Replays cost two
+    launches from the host (the position and the graph) instead of the
+    launches of the eager step (six per layer on the fused row kernels, ~15
+    without them); the recorded kernels (the row kernels and the decode
+    kernels, or hipBLASLt GEMMs, torch elementwise / reduction kernels and
+    the prologue kernel) write no memset nodes of their own."""
 
     def __init__(self, model: TS2TSModel, cache: KVCache):
-        dev = cache.k.device
         self.cache = cache
-        self.tok = torch.zeros((1, 1), dtype=torch.int64, device=dev)
-        self.pos = torch.zeros((1,), dtype=torch.int64, device=dev)
-        self.qpos = torch.zeros((1, 1), dtype=torch.int32, device=dev)
-        self.qdoc = torch.zeros((1, 1), dtype=torch.int32, device=dev)
-        self.qbits = (torch.zeros((1, cache.words, 1), dtype=torch.int64, device=dev)
-                      if cache.words else None)
+        self.pos = torch.zeros((1,), dtype=torch.int64, device=cache.k.device)
         self.model = model
         self.fused = model.fuse_rows
         self.graph = None
@@ -354,7 +377,7 @@ class _DecodeGraph:
         """Warm up on a side stream (default priority), then capture.  The
         buffers already hold the first step's values, so the warm-up run writes
         exactly what the first replay writes."""
-        dev = self.tok.device
+        dev = self.pos.device
         side = torch.cuda.Stream(device=dev)
         side.wait_stream(torch.cuda.current_stream(dev))
         with torch.cuda.stream(side):
@@ -364,13 +387,9 @@ class _DecodeGraph:
         with torch.cuda.graph(self.graph):
             self.logits = self.model._step_body(self.cache, self)
 
-    def run(self, tokens: torch.Tensor, bm, p: int) -> torch.Tensor:
-        self.tok.copy_(tokens[:, p:p + 1])
+    def run(self, p: int) -> torch.Tensor:
+        """Logits of the row at position p, whose inputs are in the cache."""
         self.pos.fill_(p)
-        self.qpos.fill_(p)
-        self.qdoc.copy_(bm.doc_ids[:, p:p + 1])
-        if self.qbits is not None:
-            self.qbits.copy_(bm.q_bits[:, :, p:p + 1])
         if self.graph is None:
             self._capture()
         self.graph.replay()

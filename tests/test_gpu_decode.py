@@ -161,6 +161,13 @@ def test_cached_generation_matches_full_recompute(graphs):
         spans = _grow(spans, 1)
         T += 1
         _check_last(m, vocab[:, :T], spans, f"decode step {step}")
+    # one token appended while an earlier one changed: the single-row step
+    # launched at once is discarded and the rows from the change recomputed
+    spans = _grow(spans, 1)
+    T += 1
+    tok = vocab[:, :T].clone()
+    tok[0, T - 10] = (tok[0, T - 10] + 7) % 500
+    _check_last(m, tok, spans, "appended + changed")
     spans = _grow(spans, 5)  # five new rows at once
     T += 5
     _check_last(m, vocab[:, :T], spans, "5-row step")

@@ -78,3 +78,38 @@ def test_training_module_signature():
                                         block_mask_creator=lambda **kw: None)
     assert m.loss_fn.weight is m.embedding.weight  # weight tying
     assert len(m.backbone.layers) == 2 and m.backbone.skip_weights.numel() == 1
+
+
+def test_token_lists_packing_clips_bounds_and_wraps_doc_ids():
+    """TokenLists packs each row's spans and grants as int32 with bounds
+    clipped to [-1, T + 1] (same coverage of [0, T)) and doc ids wrapped to
+    int32; rows with bounds beyond int64 take the per-entry path."""
+    import random
+    import numpy as np
+    from tagseq2tagseq_amd import mask_creators as mc, synth
+    rng = random.Random(0)
+    T = 1000
+    for _ in range(50):
+        B = rng.randint(1, 3)
+        spans = [[synth.DocSpan(doc_id=rng.randint(-5, 2 ** 40), start=rng.randint(-50, 1100),
+                                end=rng.randint(-50, 1100)) for _ in range(rng.randint(0, 6))]
+                 for _ in range(B)]
+        grants = [[(rng.randint(0, 127), *[rng.randint(-50, 1100) for _ in range(4)])
+                   for _ in range(rng.randint(0, 5))] for _ in range(B)]
+        if rng.random() < 0.2 and spans[0]:
+            spans[0][0] = synth.DocSpan(doc_id=1, start=-2 ** 70, end=2 ** 70)
+        got = mc.TokenLists(T, spans, torch.device("cpu"), 2, grants, None).lists.numpy()
+        ms = max(1, max(len(r) for r in spans))
+        mg = max(1, max(len(r) for r in grants))
+        sp = np.zeros((B, ms, 3), np.int64)
+        gr = np.zeros((B, mg, 5), np.int64)
+        for b, row in enumerate(spans):
+            for i, s in enumerate(row):
+                sp[b, i] = (min(max(s.start, -1), T + 1), min(max(s.end, -1), T + 1),
+                            (s.doc_id + 2 ** 31) % 2 ** 32 - 2 ** 31)
+        for b, row in enumerate(grants):
+            for i, (bit, *bounds) in enumerate(row):
+                gr[b, i] = (bit, *[min(max(x, -1), T + 1) for x in bounds])
+        cnt = np.array([[len(r) for r in spans], [len(r) for r in grants]])
+        ref = np.concatenate([sp.ravel(), gr.ravel(), cnt.ravel()]).astype(np.int32)
+        assert np.array_equal(got, ref)
