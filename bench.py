@@ -421,6 +421,77 @@ def decode_bench(args, dev):
     }))
 
 
+def rows_bench(args, dev):
+    """The fused few-row linear kernels of a decode step at the configs[4]
+    model's layer shapes (one row, d768, GLU hidden 2048, vocab 50257): each
+    kernel timed alone, algorithmic bytes = the weight matrix read once
+    (2 N K; the rows, norm weights and outputs are < 0.1 % of it).  Timed as
+    replays of a HIP graph of `--reps` calls (a ctypes call costs more host
+    time than one kernel takes); `--rows-eager` launches the calls directly
+    instead (no graph), e.g. for counter passes."""
+    from tagseq2tagseq_amd.modules import RMSNorm
+    from tagseq2tagseq_amd.rope import rope_tables
+    from tagseq2tagseq_amd.rows import rows_linear, rows_qkv_rope
+    C, hid, V, H, T = 768, 2048, 50257, 12, 16384
+    D = C // H
+    g = torch.Generator().manual_seed(args.seed)
+
+    def w(n, k):
+        return (torch.randn(n, k, generator=g) / math.sqrt(k)).to(torch.bfloat16).to(dev)
+
+    x = torch.randn(1, C, generator=g).to(torch.bfloat16).to(dev)
+    h = torch.randn(1, hid, generator=g).to(torch.bfloat16).to(dev)
+    norm = RMSNorm(C).to(dev).to(torch.bfloat16)
+    wqkv, wproj, wgu, wdown, whead = w(3 * C, C), w(C, C), w(2 * hid, C), w(C, hid), w(V, C)
+    cos, sin = rope_tables(D, T, dev)
+    kc = torch.zeros(1, H, T, D, dtype=torch.bfloat16, device=dev)
+    vc = torch.zeros_like(kc)
+    pos = torch.tensor([T - 1], dtype=torch.int64, device=dev)
+    calls = {
+        "qkv_rope (norm + qkv + rotation + cache write)":
+            (lambda: rows_qkv_rope(x, wqkv, H, cos, sin, pos, kc, vc, norm=norm), 3 * C * C),
+        "add (out-projection + residual)":
+            (lambda: rows_linear(x, wproj, epilogue="add", res=x), C * C),
+        "swiglu (norm + gate_up + SwiGLU)":
+            (lambda: rows_linear(x, wgu, norm=norm, epilogue="swiglu"), 2 * hid * C),
+        "add (down + residual)": (lambda: rows_linear(h, wdown, epilogue="add", res=x), C * hid),
+        "store (norm + LM head)": (lambda: rows_linear(x, whead, norm=norm), V * C),
+    }
+    out = {}
+    for name, (fn, n_weights) in calls.items():
+        fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        if args.rows_eager:
+            e0.record()
+            for _ in range(args.reps):
+                fn()
+            e1.record()
+        else:
+            side = torch.cuda.Stream(dev)
+            side.wait_stream(torch.cuda.current_stream(dev))
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, stream=side):
+                for _ in range(args.reps):
+                    fn()
+            graph.replay()
+            torch.cuda.synchronize()
+            e0.record()
+            graph.replay()
+            e1.record()
+        torch.cuda.synchronize()
+        us = 1e3 * e0.elapsed_time(e1) / args.reps
+        nbytes = 2 * n_weights
+        gbps = nbytes / (us * 1e-6) / 1e9
+        out[name] = {"us": round(us, 2), "weight_bytes": nbytes, "GBps": round(gbps, 1),
+                     "frac_of_hbm_peak": round(gbps / PEAK_HBM_GBS, 3)}
+    print(json.dumps({
+        "metric": "fused few-row linear kernels of a decode step (1 row, configs[4] layer shapes)",
+        "unit": "us per launch", "timing": "eager launches" if args.rows_eager else "graph replays",
+        "reps": args.reps, "dtype": "bf16", "data": "synthetic (random weights and rows)",
+        "kernels": out}))
+
+
 def config1_bench(args, dev):
     """doc_causal forward only, float32, B1 H4 T1024 D64 -- the
     reference's CPU-runnable case.  A step = per-token inputs from the span
@@ -585,6 +656,10 @@ def main():
     ap.add_argument("--decode", action="store_true",
                     help="generation with the key/value cache on the configs[4] model "
                          "(per-token latency, cached vs full recompute, decode kernel roofline)")
+    ap.add_argument("--rows", action="store_true",
+                    help="the fused few-row linear kernels of a decode step, each timed alone")
+    ap.add_argument("--rows-eager", action="store_true",
+                    help="with --rows: time direct launches instead of graph replays")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -596,6 +671,9 @@ def main():
         sys.exit(2)
     dev = torch.device("cuda:0")
 
+    if args.rows:
+        rows_bench(args, dev)
+        return
     if args.decode:
         decode_bench(args, dev)
         return

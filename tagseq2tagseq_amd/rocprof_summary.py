@@ -35,6 +35,7 @@ WORKLOADS = {
     "4": "cross_doc_link GQA B1 Hq16 Hkv4 T32768 D128 bf16",
     "5": "12-layer d768 H12 D64 backbone training step, cross_doc_link T16384 bf16",
     "decode": "generation on the config-5 model, T~16k context, one token per step",
+    "rows": "fused few-row linear kernels of a decode step, one row, config-5 layer shapes",
 }
 DEFAULT_ARGS = "--config {cfg} --no-cpu-baseline --steps 10 --warmup 3"
 
