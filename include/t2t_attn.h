@@ -305,12 +305,18 @@ int t2t_rms_norm_backward(const void *dy, int64_t dy_stride, const void *x, int6
  *            xin = bf16(x / sqrt(mean(x^2) + eps) * norm_weight), as
  *            t2t_rms_norm writes it; NULL: xin = x.
  *   res, y   bf16 rows [M][N]; y may be res (in place), nothing else may alias.
+ *   skip_weight  optional (ADD only) device scalar w (skip_weight_dtype 0 bf16,
+ *            1 float32): y = bf16(t + bf16(w * s)) with t = the add's result and
+ *            s = skip rows [M][N] (skip_stride), or s = t when skip is NULL --
+ *            the backbone's weighted skip connection
+ *            (model/modules/backbone.py:93-104) of the next layer folded in.
  * Products are summed in fp32 and rounded to bf16 before the epilogue.
  */
 int t2t_rows_linear(const void *x, int64_t x_stride, int32_t M, int32_t K, const void *weight,
                     int32_t N, const void *norm_weight, int32_t norm_dtype, float eps,
-                    int32_t epilogue, const void *res, int64_t res_stride, void *y,
-                    int64_t y_stride, void *stream);
+                    int32_t epilogue, const void *res, int64_t res_stride, const void *skip,
+                    int64_t skip_stride, const void *skip_weight, int32_t skip_weight_dtype,
+                    void *y, int64_t y_stride, void *stream);
 
 /*
  * qkv projection of a few rows with the rotary embedding and the key/value

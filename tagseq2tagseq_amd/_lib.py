@@ -66,7 +66,7 @@ _SIGS = {
     "t2t_attn_decode": ([_P] * 7 + [_I64] + [_P] * 3 + [_I32] * 9 + [ctypes.c_float, _P, _I64, _P],
                         ctypes.c_int),
     "t2t_rows_linear": ([_P, _I64, _I32, _I32, _P, _I32, _P, _I32, ctypes.c_float, _I32, _P, _I64,
-                         _P, _I64, _P], ctypes.c_int),
+                         _P, _I64, _P, _I32, _P, _I64, _P], ctypes.c_int),
     "t2t_rows_qkv_rope": ([_P, _I64, _I32, _I32, _P, _P, _I32, ctypes.c_float, _I32, _I32, _P, _P,
                            _I32, _P, _I32, _P, _P, _P, _I32, _P], ctypes.c_int),
 }

@@ -130,10 +130,13 @@ hipError_t launch_rmsnorm_bwd(const __bf16* dy, int64_t dys, const __bf16* x, in
 // RMSNorm of the input and a fused epilogue; the modes match T2T_ROWS_*.
 enum RowsMode { kRowsStore = 0, kRowsAdd = 1, kRowsSwiglu = 2, kRowsQkvRope = 3 };
 constexpr int kRowsMaxRows = 8;
+// kRowsAdd: y = res + W x, then, when skip_w is given, + skip_w * skip
+// (skip NULL: the sum itself), each step rounded to bf16.
 hipError_t launch_rows_linear(int mode, const __bf16* x, int64_t xs, int M, int K,
                               const __bf16* w, int N, const void* norm_w, bool norm_f32,
-                              float eps, const __bf16* res, int64_t rs, __bf16* y, int64_t ys,
-                              hipStream_t stream);
+                              float eps, const __bf16* res, int64_t rs, const __bf16* skip,
+                              int64_t ss, const void* skip_w, bool skip_w_f32, __bf16* y,
+                              int64_t ys, hipStream_t stream);
 // qkv projection of the rows, rotated q rows to q [H][M][D] and rotated k /
 // plain v rows to the cache views at the rows' positions (pos[m], or
 // pos0 + m when pos is NULL); positions outside [0, max_pos) are not written.

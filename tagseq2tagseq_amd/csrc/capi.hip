@@ -480,8 +480,9 @@ extern "C" {
 
 int t2t_rows_linear(const void* x, int64_t x_stride, int32_t M, int32_t K, const void* weight,
                     int32_t N, const void* norm_weight, int32_t norm_dtype, float eps,
-                    int32_t epilogue, const void* res, int64_t res_stride, void* y,
-                    int64_t y_stride, void* stream) {
+                    int32_t epilogue, const void* res, int64_t res_stride, const void* skip,
+                    int64_t skip_stride, const void* skip_weight, int32_t skip_weight_dtype,
+                    void* y, int64_t y_stride, void* stream) {
   int rc = check_rows(M, K, N, x, x_stride, weight, norm_weight, norm_dtype);
   if (rc) return rc;
   if (epilogue != T2T_ROWS_STORE && epilogue != T2T_ROWS_ADD && epilogue != T2T_ROWS_SWIGLU)
@@ -490,12 +491,24 @@ int t2t_rows_linear(const void* x, int64_t x_stride, int32_t M, int32_t K, const
   if (y_stride < N) return fail(T2T_EINVAL, "y row stride %lld is below N", (long long)y_stride);
   if (epilogue == T2T_ROWS_ADD && (!res || res_stride < N))
     return fail(T2T_EINVAL, "the add epilogue needs res with a row stride of at least N");
+  if (skip_weight) {
+    if (epilogue != T2T_ROWS_ADD)
+      return fail(T2T_EINVAL, "a skip residual is only taken by the add epilogue");
+    if (skip_weight_dtype != 0 && skip_weight_dtype != 1)
+      return fail(T2T_EUNSUPPORTED, "skip weight dtype %d (0 bf16, 1 f32)", skip_weight_dtype);
+    if (skip && skip_stride < N)
+      return fail(T2T_EINVAL, "skip row stride %lld is below N", (long long)skip_stride);
+  } else if (skip) {
+    return fail(T2T_EINVAL, "skip rows given without a skip weight");
+  }
   if (M == 0) return T2T_OK;
   return hip_status(
       t2t::launch_rows_linear(epilogue, static_cast<const __bf16*>(x), x_stride, M, K,
                               static_cast<const __bf16*>(weight), N, norm_weight, norm_dtype == 1,
                               eps, static_cast<const __bf16*>(res), res_stride,
-                              static_cast<__bf16*>(y), y_stride, static_cast<hipStream_t>(stream)),
+                              static_cast<const __bf16*>(skip), skip_stride, skip_weight,
+                              skip_weight_dtype == 1, static_cast<__bf16*>(y), y_stride,
+                              static_cast<hipStream_t>(stream)),
       "t2t_rows_linear launch");
 }
 

@@ -22,6 +22,10 @@
 // in an order of this kernel's own, so products agree with a library GEMM's
 // to bf16 rounding, not bit for bit.
 //
+// The residual add can take a second, weighted residual: the backbone's skip
+// connection (model/modules/backbone.py:93-104) that the next layer adds to
+// its input, x + w skip, folded into this layer's last product.
+//
 // Layout: W [rows][K] bf16, row-major (nn.Linear's weight); x [M][K],
 // y [M][N], res [M][N] bf16 with row strides; K % 8 == 0, K <= 4096, M <= 8.
 // A work-group is four waves.  Each wave takes R output units (an output
@@ -49,6 +53,10 @@ struct RowsArgs {
   float eps;
   const __bf16* res;   // residual rows (kRowsAdd)
   int64_t rs;
+  const __bf16* skip;  // kRowsAdd: second residual rows, or NULL for the sum itself
+  int64_t ss;
+  const void* skip_w;  // kRowsAdd: scalar weight of the second residual, or NULL for none
+  int skip_w_f32;
   __bf16* y;           // output rows (all modes but kRowsQkvRope)
   int64_t ys;
   int M, K, N;         // N: output columns; SwiGLU: hidden width; qkv: H D
@@ -221,7 +229,14 @@ __global__ __launch_bounds__(kLinThreads) void rows_linear_kernel(RowsArgs a) {
     if (MODE == kRowsStore) {
       a.y[(int64_t)m * a.ys + u] = (__bf16)sel[r];
     } else if (MODE == kRowsAdd) {
-      a.y[(int64_t)m * a.ys + u] = (__bf16)((float)a.res[(int64_t)m * a.rs + u] + bf(sel[r]));
+      float t = bf((float)a.res[(int64_t)m * a.rs + u] + bf(sel[r]));
+      if (a.skip_w) {
+        const float sw = a.skip_w_f32 ? *static_cast<const float*>(a.skip_w)
+                                      : (float)*static_cast<const __bf16*>(a.skip_w);
+        const float sk = a.skip ? (float)a.skip[(int64_t)m * a.ss + u] : t;
+        t = bf(t + bf(sw * sk));
+      }
+      a.y[(int64_t)m * a.ys + u] = (__bf16)t;
     } else if (MODE == kRowsSwiglu) {
       const float g = bf(sel[2 * r]), up = bf(sel[2 * r + 1]);
       const float act = bf(g / (1.0f + expf(-g)));
@@ -289,11 +304,13 @@ hipError_t launch_rows(int mode, const RowsArgs& a, hipStream_t stream) {
 
 hipError_t launch_rows_linear(int mode, const __bf16* x, int64_t xs, int M, int K,
                               const __bf16* w, int N, const void* norm_w, bool norm_f32,
-                              float eps, const __bf16* res, int64_t rs, __bf16* y, int64_t ys,
-                              hipStream_t stream) {
+                              float eps, const __bf16* res, int64_t rs, const __bf16* skip,
+                              int64_t ss, const void* skip_w, bool skip_w_f32, __bf16* y,
+                              int64_t ys, hipStream_t stream) {
   RowsArgs a{};
   a.x = x; a.xs = xs; a.w = w; a.norm_w = norm_w; a.norm_f32 = norm_f32; a.eps = eps;
-  a.res = res; a.rs = rs; a.y = y; a.ys = ys; a.M = M; a.K = K; a.N = N;
+  a.res = res; a.rs = rs; a.skip = skip; a.ss = ss; a.skip_w = skip_w; a.skip_w_f32 = skip_w_f32;
+  a.y = y; a.ys = ys; a.M = M; a.K = K; a.N = N;
   return launch_rows(mode, a, stream);
 }
 

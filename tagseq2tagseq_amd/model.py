@@ -252,11 +252,13 @@ class TS2TSModel:
         bb = self.backbone
         skips = []
         n_skip = len(bb.skip_weights)
+        carried = False  # this layer's skip add was folded into the previous layer
         for i, layer in enumerate(bb.layers):
-            if i >= n_skip and skips:
+            if i >= n_skip and skips and not carried:
                 x = x + bb.skip_weights[i - n_skip] * skips.pop()
             attn = layer.attn
             C = x.shape[-1]
+            nxt = self._next_skip(i, skips) if fused else None
             if fused:
                 q = rows_qkv_rope(x, attn.qkv.weight, attn.num_heads, cos_t, sin_t, buf.pos,
                                   cache.k[i], cache.v[i], norm=layer.ln_1)
@@ -266,8 +268,9 @@ class TS2TSModel:
                 cache.v[i].index_copy_(2, buf.pos, v)
             y, _ = attn_decode(q, cache.k[i], cache.v[i], cache.capacity, cache.doc,
                                cache.kv_bits if cache.words else None, qpos, qdoc, qbits)
-            x = self._layer_tail(layer, y.transpose(1, 2).reshape(1, 1, C), x, fused)
-            if i < n_skip:
+            x = self._layer_tail(layer, y.transpose(1, 2).reshape(1, 1, C), x, fused, nxt)
+            carried = nxt is not None
+            if i < n_skip and not carried:
                 skips.append(x)
         if fused:
             return rows_linear(x, self.lm_head_weight, norm=self.norm)
@@ -295,17 +298,34 @@ class TS2TSModel:
                 return False
         return isinstance(self.norm, RMSNorm)
 
+    def _next_skip(self, i: int, skips: list):
+        """The skip add that starts layer i + 1 (model/modules/backbone.py:93-104:
+        x + skip_weights[j - n_skip] * skips.pop() for layers j >= n_skip),
+        to be folded into layer i's down-projection: (rows, weight), rows None
+        when layer i + 1 pops layer i's own output; None when layer i + 1 adds
+        nothing or layer i's down-projection is not a row kernel."""
+        bb = self.backbone
+        n_skip, j = len(bb.skip_weights), i + 1
+        if j >= len(bb.layers) or j < n_skip or bb.layers[i].mlp.down.weight.shape[1] % 8:
+            return None
+        if i == n_skip - 1:
+            return None, bb.skip_weights[0]
+        if not skips:
+            return None
+        return skips.pop(), bb.skip_weights[j - n_skip]
+
     @staticmethod
-    def _layer_tail(layer, y, x, fused: bool):
+    def _layer_tail(layer, y, x, fused: bool, skip=None):
         """Out-projection + residual, norm + GLU + residual of Layer.forward
-        (model/modules/layer.py:33-34) on the attention rows y."""
+        (model/modules/layer.py:33-34) on the attention rows y; ``skip``: the
+        next layer's skip add, folded into the last product (fused only)."""
         if fused:
             mlp = layer.mlp
             x = rows_linear(y, layer.attn.proj.weight, epilogue="add", res=x)
             h = rows_linear(x, mlp.gate_up.weight, norm=layer.ln_2, epilogue="swiglu")
             if h.shape[-1] % 8:  # rows the kernel cannot read as 16-byte vectors
                 return x + mlp.down(h)
-            return rows_linear(h, mlp.down.weight, epilogue="add", res=x)
+            return rows_linear(h, mlp.down.weight, epilogue="add", res=x, skip=skip)
         x = x + layer.drop_path(layer.attn.proj(y))
         return x + layer.drop_path(layer.mlp(layer.ln_2(x)))
 
@@ -316,16 +336,19 @@ class TS2TSModel:
         skips = []
         n_skip = len(bb.skip_weights)
         fused = not full and self._rows_fusable(x)
+        carried = False  # this layer's skip add was folded into the previous layer
         for i, layer in enumerate(bb.layers):
-            if i >= n_skip and skips:
+            if i >= n_skip and skips and not carried:
                 x = x + bb.skip_weights[i - n_skip] * skips.pop()
-            x = self._layer_rows(i, layer, x, bm, cache, p0, full, fused)
-            if i < n_skip:
+            nxt = self._next_skip(i, skips) if fused else None
+            x = self._layer_rows(i, layer, x, bm, cache, p0, full, fused, nxt)
+            carried = nxt is not None
+            if i < n_skip and not carried:
                 skips.append(x)
         return x
 
     def _layer_rows(self, i: int, layer, x, bm, cache: KVCache, p0: int, full: bool,
-                    fused: bool):
+                    fused: bool, skip=None):
         """Layer.forward (model/modules/layer.py:32-35) over the new rows."""
         attn = layer.attn
         B, n, C = x.shape
@@ -351,7 +374,7 @@ class TS2TSModel:
                             cache.kv_bits if bm.words else None, pos[:, c0:c1].contiguous(),
                             bm.doc_ids[:, p0 + c0:p0 + c1].contiguous(), qb,
                             out=y[:, :, c0:c1])
-        return self._layer_tail(layer, y.transpose(1, 2).reshape(B, n, C), x, fused)
+        return self._layer_tail(layer, y.transpose(1, 2).reshape(B, n, C), x, fused, skip)
 
 
 class _DecodeGraph:

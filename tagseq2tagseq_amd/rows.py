@@ -60,14 +60,16 @@ def _stream(x: torch.Tensor) -> ctypes.c_void_p:
 
 
 def rows_linear(x: torch.Tensor, weight: torch.Tensor, *, norm=None, epilogue: str = "store",
-                res: Optional[torch.Tensor] = None,
+                res: Optional[torch.Tensor] = None, skip=None,
                 out: Optional[torch.Tensor] = None) -> torch.Tensor:
     """``epilogue(W · norm(x))`` for the rows of x [..., K] (at most 8 rows).
 
     weight: nn.Linear weight [N, K] ([2N, K] for "swiglu": gate rows then up
     rows); norm: an RMSNorm module (its ``weight`` and ``eps``) applied to x
     first, or None; res: rows [..., N] added for "add" (``out`` may be
-    ``res``).  Returns [..., N] bf16."""
+    ``res``); skip: for "add", ``(rows or None, w)`` with w a one-element
+    device tensor: the sum t then becomes t + w * rows (rows None: t + w * t),
+    the backbone's weighted skip connection.  Returns [..., N] bf16."""
     if not weight.is_contiguous():
         raise ValueError("weight must be contiguous ([N, K] row-major)")
     K = x.shape[-1]
@@ -84,11 +86,22 @@ def rows_linear(x: torch.Tensor, weight: torch.Tensor, *, norm=None, epilogue: s
     if y.stride(1) != 1:
         raise ValueError("out rows must have unit stride")
     nw, ndt, eps = _norm_args(norm)
+    sk = sw = None
+    if skip is not None:
+        sk, sw = skip
+        if sw.numel() != 1 or sw.dtype not in _WDT or not sw.is_cuda:
+            raise ValueError("the skip weight must be a one-element bf16 / float32 device tensor")
+        if sk is not None:
+            sk = sk.reshape(M, N)
+            if sk.stride(1) != 1:
+                raise ValueError("skip rows must have unit stride")
     with torch.cuda.device(x.device):
         rc = _lib.lib().t2t_rows_linear(
             xr.data_ptr(), xr.stride(0), M, K, weight.data_ptr(), N, nw, ndt, eps,
             _EPILOGUES[epilogue], rr.data_ptr() if rr is not None else None,
-            rr.stride(0) if rr is not None else 0, y.data_ptr(), y.stride(0), _stream(x))
+            rr.stride(0) if rr is not None else 0, sk.data_ptr() if sk is not None else None,
+            sk.stride(0) if sk is not None else 0, sw.data_ptr() if sw is not None else None,
+            _WDT[sw.dtype] if sw is not None else 0, y.data_ptr(), y.stride(0), _stream(x))
     _lib.check(rc, "t2t_rows_linear")
     return y.view(*x.shape[:-1], N)
 

@@ -89,6 +89,28 @@ def test_rows_linear_strided_rows_and_in_place_add():
     _assert_close(res, ref, "in-place add")
 
 
+@pytest.mark.parametrize("M", [1, 3])
+@pytest.mark.parametrize("wdt", [torch.bfloat16, torch.float32])
+def test_rows_linear_add_with_skip(M, wdt):
+    """The add epilogue with the backbone's weighted skip connection folded in:
+    t = res + W x, then t + w * skip (skip rows), or t + w * t (no rows), each
+    step rounded to bf16 as the unfused torch ops round it."""
+    g = torch.Generator().manual_seed(11 + M)
+    K, N = 2048, 768
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16).to(DEV)
+    w = (torch.randn(N, K, generator=g) / math.sqrt(K)).to(torch.bfloat16).to(DEV)
+    res = torch.randn(M, N, generator=g).to(torch.bfloat16).to(DEV)
+    sk = torch.randn(M, N, generator=g).to(torch.bfloat16).to(DEV)
+    sw = torch.tensor([0.0, 0.75, 1.3], dtype=wdt, device=DEV)[1:]  # a view at an offset
+    t = (res.float() + _lin_ref(x, w).float()).to(torch.bfloat16)
+    got = rows_linear(x, w, epilogue="add", res=res, skip=(sk, sw[1]))
+    ref = (t.float() + (sw[1].float() * sk.float()).to(torch.bfloat16).float()).to(torch.bfloat16)
+    _assert_close(got, ref, "skip rows")
+    got = rows_linear(x, w, epilogue="add", res=res, skip=(None, sw[0]))
+    ref = (t.float() + (sw[0].float() * t.float()).to(torch.bfloat16).float()).to(torch.bfloat16)
+    _assert_close(got, ref, "self skip")
+
+
 def test_rows_linear_lm_head_width():
     """A vocabulary-wide product (N = 50257, the bench model's LM head) with
     the final norm fused in."""

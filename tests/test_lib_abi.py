@@ -221,8 +221,9 @@ def test_rows_linear_argument_checks():
     P = ctypes.c_void_p(0x1000)
 
     def lin(M=1, K=768, N=768, x=P, xs=768, w=P, nw=None, ndt=0, ep=0, res=None, rs=0, y=P,
-            ys=768):
-        return lib.t2t_rows_linear(x, xs, M, K, w, N, nw, ndt, 1e-6, ep, res, rs, y, ys, None)
+            ys=768, sk=None, sks=0, sw=None, swdt=0):
+        return lib.t2t_rows_linear(x, xs, M, K, w, N, nw, ndt, 1e-6, ep, res, rs, sk, sks, sw,
+                                   swdt, y, ys, None)
 
     assert lin(M=9) == -2 and "rows" in _err()
     assert lin(M=-1) == -2
@@ -239,6 +240,11 @@ def test_rows_linear_argument_checks():
     assert lin(ep=1) == -1 and "res" in _err()
     assert lin(ep=1, res=P, rs=100) == -1
     assert lin(M=0) == 0  # nothing to do, nothing launched
+    assert lin(sw=P) == -1 and "add epilogue" in _err()
+    assert lin(ep=1, res=P, rs=768, sk=P, sks=768) == -1 and "without a skip weight" in _err()
+    assert lin(ep=1, res=P, rs=768, sw=P, swdt=2) == -2 and "dtype" in _err()
+    assert lin(ep=1, res=P, rs=768, sk=P, sks=700, sw=P) == -1 and "skip row stride" in _err()
+    assert lin(M=0, ep=1, res=P, rs=768, sk=P, sks=768, sw=P) == 0
 
     v = _dummy_view()
 
