@@ -342,6 +342,23 @@ int t2t_rows_qkv_rope(const void *x, int64_t x_stride, int32_t M, int32_t K, con
                       const t2t_tensor *k_cache, const t2t_tensor *v_cache, int32_t cache_rows,
                       void *stream);
 
+/*
+ * First position p < n at which two copies of a sequence's per-token inputs
+ * differ -- token ids, doc ids, or any q / kv grant word -- or n when they
+ * agree: the check of the generation key/value cache against the inputs of
+ * a new TS2TSModel.forward_inference_last call (no counterpart in the
+ * reference, which recomputes every position per token: generation_loop.py:90-92).
+ *   tokens_*  int64[n], doc_* int32[n], q_bits_* / kv_bits_* uint64
+ *             [words][bits_stride_*] (bits_stride >= n; NULL when words == 0).
+ *   out       int32[1] (device), written with the result.
+ * One work-group; 0 <= words <= T2T_MAX_WORDS.
+ */
+int t2t_first_input_diff(const int64_t *tokens_a, const int64_t *tokens_b, const int32_t *doc_a,
+                         const int32_t *doc_b, const uint64_t *q_bits_a, const uint64_t *q_bits_b,
+                         const uint64_t *kv_bits_a, const uint64_t *kv_bits_b,
+                         int64_t bits_stride_a, int64_t bits_stride_b, int32_t words, int32_t n,
+                         int32_t *out, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

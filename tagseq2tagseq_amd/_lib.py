@@ -67,6 +67,7 @@ _SIGS = {
                         ctypes.c_int),
     "t2t_rows_linear": ([_P, _I64, _I32, _I32, _P, _I32, _P, _I32, ctypes.c_float, _I32, _P, _I64,
                          _P, _I64, _P, _I32, _P, _I64, _P], ctypes.c_int),
+    "t2t_first_input_diff": ([_P] * 8 + [_I64, _I64, _I32, _I32, _P, _P], ctypes.c_int),
     "t2t_rows_qkv_rope": ([_P, _I64, _I32, _I32, _P, _P, _I32, ctypes.c_float, _I32, _I32, _P, _P,
                            _I32, _P, _I32, _P, _P, _P, _I32, _P], ctypes.c_int),
 }

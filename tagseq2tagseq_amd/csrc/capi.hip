@@ -541,4 +541,27 @@ int t2t_rows_qkv_rope(const void* x, int64_t x_stride, int32_t M, int32_t K, con
       "t2t_rows_qkv_rope launch");
 }
 
+int t2t_first_input_diff(const int64_t* tokens_a, const int64_t* tokens_b, const int32_t* doc_a,
+                         const int32_t* doc_b, const uint64_t* q_bits_a, const uint64_t* q_bits_b,
+                         const uint64_t* kv_bits_a, const uint64_t* kv_bits_b,
+                         int64_t bits_stride_a, int64_t bits_stride_b, int32_t words, int32_t n,
+                         int32_t* out, void* stream) {
+  if (n < 0 || words < 0 || words > T2T_MAX_WORDS)
+    return fail(T2T_EINVAL, "n = %d, words = %d (0 to %d)", n, words, T2T_MAX_WORDS);
+  if (!out) return fail(T2T_EINVAL, "out is NULL");
+  if (n > 0 && (!tokens_a || !tokens_b || !doc_a || !doc_b))
+    return fail(T2T_EINVAL, "token or doc array is NULL");
+  if (n > 0 && words > 0) {
+    if (!q_bits_a || !q_bits_b || !kv_bits_a || !kv_bits_b)
+      return fail(T2T_EINVAL, "a grant-word array is NULL");
+    if (bits_stride_a < n || bits_stride_b < n)
+      return fail(T2T_EINVAL, "grant-word stride below n");
+  }
+  return hip_status(t2t::launch_first_input_diff(tokens_a, tokens_b, doc_a, doc_b, q_bits_a,
+                                                 q_bits_b, kv_bits_a, kv_bits_b, bits_stride_a,
+                                                 bits_stride_b, words, n, out,
+                                                 static_cast<hipStream_t>(stream)),
+                    "t2t_first_input_diff launch");
+}
+
 }  // extern "C"

@@ -22,12 +22,14 @@ block-mask kernels and the cache refilled.
 """
 from __future__ import annotations
 
+import ctypes
 from typing import Any, Callable, List, Optional
 
 import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
+from . import _lib
 from .attention import flex_attention
 from .block_mask import T2TBlockMask, build_block_mask
 from .decode import MAX_ROWS, attn_decode
@@ -55,26 +57,36 @@ class KVCache:
         self.words = words
         self.length = 0
 
+    def first_diff(self, tokens: torch.Tensor, bm, n: int) -> torch.Tensor:
+        """Device int32 [1]: the first of positions 0 .. n - 1 whose token id
+        or mask inputs (doc id, q / kv words) differ from the cached ones, or n
+        (``t2t_first_input_diff``, one launch, no host sync)."""
+        out = torch.empty(1, dtype=torch.int32, device=self.tokens.device)
+
+        def row(t):
+            t = t[0]
+            return t if t.stride(-1) == 1 else t.contiguous()
+
+        tok, doc = row(tokens.to(torch.int64)), row(bm.doc_ids.to(torch.int32))
+        qa = ka = qb = kb = None
+        if self.words:
+            qa, ka, qb, kb = (row(t) for t in (self.q_bits, self.kv_bits, bm.q_bits, bm.kv_bits))
+            if qb.stride(0) != kb.stride(0):
+                qb, kb = qb.contiguous(), kb.contiguous()
+        ptr = lambda t: t.data_ptr() if t is not None else None  # noqa: E731
+        with torch.cuda.device(out.device):
+            rc = _lib.lib().t2t_first_input_diff(
+                self.tokens.data_ptr(), tok.data_ptr(), self.doc.data_ptr(), doc.data_ptr(),
+                ptr(qa), ptr(qb), ptr(ka), ptr(kb), qa.stride(0) if qa is not None else 0,
+                qb.stride(0) if qb is not None else 0, self.words, n, out.data_ptr(),
+                ctypes.c_void_p(torch.cuda.current_stream(out.device).cuda_stream))
+        _lib.check(rc, "t2t_first_input_diff")
+        return out
+
     def reusable_prefix(self, tokens: torch.Tensor, bm) -> int:
         """Length of the longest prefix whose token ids and mask inputs match."""
         n = min(self.length, tokens.shape[1])
-        if n == 0:
-            return 0
-        diff = (self.tokens[0, :n] != tokens[0, :n]) | (self.doc[0, :n] != bm.doc_ids[0, :n])
-        if self.words:
-            diff |= (self.q_bits[0, :, :n] != bm.q_bits[0, :, :n]).any(0)
-            diff |= (self.kv_bits[0, :, :n] != bm.kv_bits[0, :, :n]).any(0)
-        idx = torch.nonzero(diff)
-        return int(idx[0, 0]) if idx.numel() else n
-
-    def prefix_changed(self, tokens: torch.Tensor, bm, n: int) -> torch.Tensor:
-        """Device bool: whether the token id or a mask input of any of the
-        first n positions differs from the cached ones (no host sync)."""
-        d = (self.tokens[0, :n] != tokens[0, :n]).any() | (self.doc[0, :n] != bm.doc_ids[0, :n]).any()
-        if self.words:
-            d |= (self.q_bits[0, :, :n] != bm.q_bits[0, :, :n]).any()
-            d |= (self.kv_bits[0, :, :n] != bm.kv_bits[0, :, :n]).any()
-        return d
+        return int(self.first_diff(tokens, bm, n).item()) if n else 0
 
     def store_inputs(self, tokens: torch.Tensor, bm, p0: int, p1: int) -> None:
         self.tokens[0, p0:p1] = tokens[0, p0:p1]
@@ -199,12 +211,12 @@ class TS2TSModel:
             # step's launches, so the step costs one host synchronisation.
             cache.store_inputs(tokens, bm, p, T)
             logits = self._graph_step(cache, tokens, bm, p)
-            changed = cache.prefix_changed(tokens, bm, p)  # reads positions < p only
-            if not bool(changed):
+            first = cache.first_diff(tokens, bm, p)  # reads positions < p only
+            if int(first.item()) == p:
                 cache.length = T
                 return logits
             # an earlier input changed: recompute from the first difference
-            cache.length = p
+            cache.length = int(first.item())
         p0 = min(cache.reusable_prefix(tokens, bm), T - 1)
         full = T - p0 > self.prefill_rows
         if full:

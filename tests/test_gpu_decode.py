@@ -273,3 +273,50 @@ def test_fused_row_kernels_match_unfused_layers(graphs, dim, heads, monkeypatch)
         err = (fused - plain).abs().max().item()
         assert err <= 2e-2 * scale + 1e-3, f"{n} rows: max err {err:.4g} (scale {scale:.3g})"
     assert calls, "the fused row kernels did not run"
+
+
+@pytest.mark.parametrize("words", [0, 1, 3])
+def test_first_input_diff_kernel(words):
+    """t2t_first_input_diff (the cache check) against numpy: the first position
+    whose token id, doc id or any q / kv word differs, or n; a difference
+    planted in each array in turn, at positions across the work-group's
+    steps, n = 0 and n not a multiple of the group size; bits rows with a
+    stride above n."""
+    from tagseq2tagseq_amd.model import KVCache
+    rng = np.random.default_rng(words)
+    cap, n_tot = 9000, 8195
+    cache = KVCache(1, 1, 64, cap, words, DEV)
+    tok = rng.integers(0, 500, (1, n_tot))
+    doc = rng.integers(0, 9, (1, n_tot)).astype(np.int32)
+    qb = rng.integers(0, 2 ** 62, (1, words, n_tot))
+    kb = rng.integers(0, 2 ** 62, (1, words, n_tot))
+
+    class Inputs:
+        pass
+
+    cache.tokens[0, :n_tot] = torch.from_numpy(tok[0]).to(DEV)
+    cache.doc[0, :n_tot] = torch.from_numpy(doc[0]).to(DEV)
+    if words:
+        cache.q_bits[0, :, :n_tot] = torch.from_numpy(qb[0]).to(DEV)
+        cache.kv_bits[0, :, :n_tot] = torch.from_numpy(kb[0]).to(DEV)
+    arrays = ["tok", "doc"] + (["q", "kv"] if words else [])
+    cases = [(None, None)] + [(a, p) for a in arrays for p in (0, 1023, 1024, 4097, 8194)]
+    for which, p in cases:
+        t2, d2, q2, k2 = tok.copy(), doc.copy(), qb.copy(), kb.copy()
+        if which == "tok":
+            t2[0, p] += 1
+        elif which == "doc":
+            d2[0, p] += 1
+        elif which == "q":
+            q2[0, words - 1, p] ^= 1 << 40
+        elif which == "kv":
+            k2[0, 0, p] ^= 1
+        bm = Inputs()
+        bm.doc_ids = torch.from_numpy(d2).to(DEV)
+        bm.q_bits = torch.from_numpy(q2).to(DEV)
+        bm.kv_bits = torch.from_numpy(k2).to(DEV)
+        toks = torch.from_numpy(t2).to(DEV)
+        for n in (n_tot, 4096, 1, 0):
+            want = p if p is not None and p < n else n
+            got = int(cache.first_diff(toks, bm, n).item())
+            assert got == want, f"{which} at {p}, n={n}: got {got}, want {want}"

@@ -260,3 +260,15 @@ def test_rows_linear_argument_checks():
     bad = _lib.T2TTensor(0, 0, 0, 64)
     assert qkv(views=(v, bad, v)) == -1 and "view" in _err()
     assert qkv(M=0) == 0
+
+
+def test_first_input_diff_argument_checks():
+    lib = _lib.lib()
+    P = ctypes.c_void_p(0x1000)
+    args = lambda words=1, n=16, out=P, sa=16, sb=16, q=P: (  # noqa: E731
+        P, P, P, P, q, q, q, q, sa, sb, words, n, out, None)
+    assert lib.t2t_first_input_diff(*args(words=9)) == -1 and "words" in _err()
+    assert lib.t2t_first_input_diff(*args(n=-1)) == -1
+    assert lib.t2t_first_input_diff(*args(out=None)) == -1 and "out" in _err()
+    assert lib.t2t_first_input_diff(*args(q=None)) == -1 and "grant-word" in _err()
+    assert lib.t2t_first_input_diff(*args(sa=8)) == -1 and "stride" in _err()
