@@ -297,8 +297,10 @@ int t2t_rms_norm_backward(const void *dy, int64_t dy_stride, const void *x, int6
  * (model/modules/layer.py:32-35: tunalab FlexSelfAttention's out-projection,
  * GLU's gate_up and down, and the head's lm_head at model/model.py:227-237)
  * together with the RMSNorm before them and the residual add or SwiGLU after.
- *   x        bf16 rows [M][K] (row stride x_stride, elements); K % 8 == 0,
- *            K <= 4096, 0 <= M <= 8; 16-byte aligned.
+ *   x        bf16 rows [M][K] (row stride x_stride >= K, elements); 1 <= K <=
+ *            4096, 0 <= M <= 8; rows are read as 16-byte vectors when K and
+ *            x_stride are multiples of 8 and x, weight (and a float32 norm
+ *            weight) are 16-byte aligned, element by element otherwise.
  *   weight   bf16 [N][K] row-major (nn.Linear layout); [2N][K] for SWIGLU
  *            (gate rows, then up rows: the gate_up output chunked in two).
  *   norm_weight  optional RMSNorm weight [K] (norm_dtype 0 bf16, 1 float32):

@@ -456,20 +456,17 @@ int check_rows(int M, int K, int N, const void* x, int64_t x_stride, const void*
                const void* norm_weight, int norm_dtype) {
   if (M < 0 || M > t2t::kRowsMaxRows)
     return fail(T2T_EUNSUPPORTED, "M = %d rows; 0 to %d supported", M, t2t::kRowsMaxRows);
-  if (K < 8 || K > 4096 || K % 8)
-    return fail(T2T_EUNSUPPORTED, "K = %d is not a multiple of 8 in [8, 4096]", K);
+  if (K < 1 || K > 4096) return fail(T2T_EUNSUPPORTED, "K = %d outside [1, 4096]", K);
   if (N < 1) return fail(T2T_EINVAL, "N = %d", N);
   if (!x || !weight) return fail(T2T_EINVAL, "x or weight is NULL");
-  if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(weight)) % 16)
-    return fail(T2T_EINVAL, "x and weight must be 16-byte aligned");
-  if (x_stride < K || x_stride % 8)
-    return fail(T2T_EINVAL, "x row stride %lld is below K or not a multiple of 8",
-                (long long)x_stride);
+  if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(weight)) % 2)
+    return fail(T2T_EINVAL, "x and weight must be 2-byte aligned");
+  if (x_stride < K) return fail(T2T_EINVAL, "x row stride %lld is below K", (long long)x_stride);
   if (norm_weight) {
     if (norm_dtype != 0 && norm_dtype != 1)
       return fail(T2T_EUNSUPPORTED, "norm weight dtype %d (0 bf16, 1 f32)", norm_dtype);
-    if (reinterpret_cast<uintptr_t>(norm_weight) % 16)
-      return fail(T2T_EINVAL, "norm weight must be 16-byte aligned");
+    if (reinterpret_cast<uintptr_t>(norm_weight) % (norm_dtype ? 4 : 2))
+      return fail(T2T_EINVAL, "norm weight misaligned for its dtype");
   }
   return T2T_OK;
 }

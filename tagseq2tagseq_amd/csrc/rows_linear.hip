@@ -27,7 +27,10 @@
 // its input, x + w skip, folded into this layer's last product.
 //
 // Layout: W [rows][K] bf16, row-major (nn.Linear's weight); x [M][K],
-// y [M][N], res [M][N] bf16 with row strides; K % 8 == 0, K <= 4096, M <= 8.
+// y [M][N], res [M][N] bf16 with row strides; K <= 4096, M <= 8.  Rows are
+// read in 16-byte vectors when K, the x row stride and the pointers allow it,
+// else element by element (e.g. the GLU hidden width int(8/3 C) = 1365 for
+// C = 512), with the chunk past K read as zero.
 // A work-group is four waves.  Each wave takes R output units (an output
 // column; for SwiGLU the (gate, up) row pair; for the qkv mode the rotation
 // pair (i, i + D/2) of one head's q, k or v rows) and issues every 16-byte
@@ -60,6 +63,7 @@ struct RowsArgs {
   __bf16* y;           // output rows (all modes but kRowsQkvRope)
   int64_t ys;
   int M, K, N;         // N: output columns; SwiGLU: hidden width; qkv: H D
+  int aligned;         // K, the row strides and pointers allow 16-byte row loads
   // kRowsQkvRope: q rows [H][M][D] (the views' t axis), k / v cache rows at
   // the rows' positions, cos / sin tables [table_rows][D / 2].
   const float* cos;
@@ -75,7 +79,28 @@ __device__ __forceinline__ float wave_sum(float x) {
   return x;
 }
 
-__device__ __forceinline__ void norm_weight8(const void* w, int f32, int v, float (&out)[8]) {
+// Elements 8c .. 8c + 7 of a row of K, zero past K: one 16-byte load when the
+// rows are 16-byte aligned, else element loads.
+__device__ __forceinline__ bf16x8 load8(const __bf16* row, int c, int K, int aligned) {
+  if (aligned) return reinterpret_cast<const bf16x8*>(row)[c];
+  bf16x8 v;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) v[e] = 8 * c + e < K ? row[8 * c + e] : (__bf16)0.f;
+  return v;
+}
+
+__device__ __forceinline__ void norm_weight8(const void* w, int f32, int v, float (&out)[8],
+                                             int K, int aligned) {
+  if (!aligned) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int i = 8 * v + e;
+      out[e] = i >= K ? 0.f
+                      : (f32 ? static_cast<const float*>(w)[i]
+                             : (float)static_cast<const __bf16*>(w)[i]);
+    }
+    return;
+  }
   if (f32) {
     const float4 a = reinterpret_cast<const float4*>(w)[2 * v];
     const float4 b = reinterpret_cast<const float4*>(w)[2 * v + 1];
@@ -120,7 +145,7 @@ __global__ __launch_bounds__(kLinThreads) void rows_linear_kernel(RowsArgs a) {
   constexpr int NW = P * R;
   extern __shared__ bf16x8 xl[];  // [MT][K / 8]
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int nv = a.K >> 3;
+  const int nv = (a.K + 7) >> 3;
   const int nunits = unit_count(MODE, a.N);
   const int u0 = (blockIdx.x * kLinWaves + wave) * R;
 
@@ -131,12 +156,11 @@ __global__ __launch_bounds__(kLinThreads) void rows_linear_kernel(RowsArgs a) {
 #pragma unroll
     for (int s = 0; s < P; ++s) {
       const bool ok = u0 + r < nunits;
-      const bf16x8* wr =
-          reinterpret_cast<const bf16x8*>(a.w + (int64_t)(ok ? weight_row<MODE>(a, u0 + r, s) : 0) * a.K);
+      const __bf16* wr = a.w + (int64_t)(ok ? weight_row<MODE>(a, u0 + r, s) : 0) * a.K;
 #pragma unroll
       for (int k = 0; k < KV; ++k) {
         const int c = lane + 64 * k;
-        wv[r * P + s][k] = (ok && c < nv) ? wr[c] : bf16x8{};
+        wv[r * P + s][k] = (ok && c < nv) ? load8(wr, c, a.K, a.aligned) : bf16x8{};
       }
     }
 
@@ -150,13 +174,13 @@ __global__ __launch_bounds__(kLinThreads) void rows_linear_kernel(RowsArgs a) {
         if (lane + 64 * k < nv) dst[lane + 64 * k] = bf16x8{};
       continue;
     }
-    const bf16x8* xr = reinterpret_cast<const bf16x8*>(a.x + (int64_t)m * a.xs);
+    const __bf16* xr = a.x + (int64_t)m * a.xs;
     bf16x8 xv[KV];
     float ss = 0.f;
 #pragma unroll
     for (int k = 0; k < KV; ++k) {
       const int c = lane + 64 * k;
-      xv[k] = c < nv ? xr[c] : bf16x8{};
+      xv[k] = c < nv ? load8(xr, c, a.K, a.aligned) : bf16x8{};
 #pragma unroll
       for (int e = 0; e < 8; ++e) ss = fmaf((float)xv[k][e], (float)xv[k][e], ss);
     }
@@ -167,7 +191,7 @@ __global__ __launch_bounds__(kLinThreads) void rows_linear_kernel(RowsArgs a) {
         const int c = lane + 64 * k;
         if (c < nv) {
           float nw[8];
-          norm_weight8(a.norm_w, a.norm_f32, c, nw);
+          norm_weight8(a.norm_w, a.norm_f32, c, nw, a.K, a.aligned);
           bf16x8 o;
 #pragma unroll
           for (int e = 0; e < 8; ++e) o[e] = (__bf16)((float)xv[k][e] * rr * nw[e]);
@@ -268,7 +292,7 @@ hipError_t launch_kmm(const RowsArgs& a, hipStream_t stream) {
   constexpr int per_wg = kLinWaves * units_per_wave<KV, MODE>();
   const int units = unit_count(MODE, a.N);
   const dim3 grid((unsigned)((units + per_wg - 1) / per_wg));
-  const size_t lds = (size_t)MT * (a.K / 8) * sizeof(bf16x8);
+  const size_t lds = (size_t)MT * ((a.K + 7) / 8) * sizeof(bf16x8);
   hipLaunchKernelGGL((rows_linear_kernel<KV, MT, MODE>), grid, dim3(kLinThreads), lds, stream,
                      a);
   return hipGetLastError();
@@ -292,8 +316,11 @@ hipError_t launch_k(int mode, const RowsArgs& a, hipStream_t stream) {
   return launch_km<KV, 8>(mode, a, stream);
 }
 
-hipError_t launch_rows(int mode, const RowsArgs& a, hipStream_t stream) {
-  const int nv = a.K / 8;
+hipError_t launch_rows(int mode, RowsArgs a, hipStream_t stream) {
+  const int nv = (a.K + 7) / 8;
+  const uintptr_t ptrs = reinterpret_cast<uintptr_t>(a.x) | reinterpret_cast<uintptr_t>(a.w) |
+                         reinterpret_cast<uintptr_t>(a.norm_w);
+  a.aligned = a.K % 8 == 0 && a.xs % 8 == 0 && ptrs % 16 == 0;
   if (nv <= 64) return launch_k<1>(mode, a, stream);
   if (nv <= 128) return launch_k<2>(mode, a, stream);
   if (nv <= 256) return launch_k<4>(mode, a, stream);

@@ -315,10 +315,10 @@ class TS2TSModel:
         x + skip_weights[j - n_skip] * skips.pop() for layers j >= n_skip),
         to be folded into layer i's down-projection: (rows, weight), rows None
         when layer i + 1 pops layer i's own output; None when layer i + 1 adds
-        nothing or layer i's down-projection is not a row kernel."""
+        nothing."""
         bb = self.backbone
         n_skip, j = len(bb.skip_weights), i + 1
-        if j >= len(bb.layers) or j < n_skip or bb.layers[i].mlp.down.weight.shape[1] % 8:
+        if j >= len(bb.layers) or j < n_skip:
             return None
         if i == n_skip - 1:
             return None, bb.skip_weights[0]
@@ -335,8 +335,6 @@ class TS2TSModel:
             mlp = layer.mlp
             x = rows_linear(y, layer.attn.proj.weight, epilogue="add", res=x)
             h = rows_linear(x, mlp.gate_up.weight, norm=layer.ln_2, epilogue="swiglu")
-            if h.shape[-1] % 8:  # rows the kernel cannot read as 16-byte vectors
-                return x + mlp.down(h)
             return rows_linear(h, mlp.down.weight, epilogue="add", res=x, skip=skip)
         x = x + layer.drop_path(layer.attn.proj(y))
         return x + layer.drop_path(layer.mlp(layer.ln_2(x)))

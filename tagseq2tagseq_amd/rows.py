@@ -33,17 +33,17 @@ _WDT = {torch.bfloat16: 0, torch.float32: 1}
 
 
 def applies(x: torch.Tensor, *weights: torch.Tensor) -> bool:
-    """bf16 rows on a GPU, at most ``ROWS_MAX`` of them, bf16 weights."""
+    """bf16 rows on a GPU, at most ``ROWS_MAX`` of them and at most 4096 wide,
+    bf16 weights."""
     rows = x.numel() // max(1, x.shape[-1])
     return (x.is_cuda and x.dtype == torch.bfloat16 and 0 < rows <= _lib.ROWS_MAX
-            and x.shape[-1] % 8 == 0 and x.shape[-1] <= 4096
+            and 0 < x.shape[-1] <= 4096
             and all(w.dtype == torch.bfloat16 and w.is_cuda for w in weights))
 
 
 def _rows(t: torch.Tensor) -> torch.Tensor:
     t = t.reshape(-1, t.shape[-1])
-    ok = t.stride(1) == 1 and t.stride(0) % 8 == 0 and t.data_ptr() % 16 == 0
-    return t if ok else t.contiguous()
+    return t if t.stride(1) == 1 and t.stride(0) >= t.shape[1] else t.contiguous()
 
 
 def _norm_args(norm):

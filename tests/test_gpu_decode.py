@@ -120,8 +120,8 @@ def test_too_many_rows_raises():
 # -- cached model path ------------------------------------------------------
 
 def _model(creator, T_max=1024):
-    # model_dim 384: GLU hidden width 1024, a multiple of 8, so few-row steps
-    # run on the fused row kernels
+    # model_dim 384: GLU hidden width 1024, a multiple of 8, so the row
+    # kernels read every operand in 16-byte vectors
     torch.manual_seed(0)
     m = TS2TSModel.from_config(vocab_size=500, num_layers=4, model_dim=384, num_heads=6,
                                max_seq_len=T_max, dropout=0.0, drop_path_rate=0.0,
@@ -240,8 +240,8 @@ def test_fused_row_kernels_match_unfused_layers(graphs, dim, heads, monkeypatch)
     write, out-projection + residual, norm + gate_up + SwiGLU, down +
     residual, norm + LM head) against the same steps through the unfused torch
     layer sequence, one and five rows at a time.  dim 256 has a GLU hidden
-    width of 682, not a multiple of 8: its down-projection stays a torch
-    product, the rest is fused."""
+    width of 682, not a multiple of 8: its down-projection reads its rows
+    element by element instead of in 16-byte vectors."""
     import tagseq2tagseq_amd.model as model_mod
     calls = []
     real = model_mod.rows_linear

@@ -51,7 +51,8 @@ def _norm(K, dtype, seed):
 
 
 @pytest.mark.parametrize("M", [1, 2, 3, 5, 8])
-@pytest.mark.parametrize("K,N", [(64, 40), (768, 768), (768, 1001), (2048, 768), (4096, 264)])
+@pytest.mark.parametrize("K,N", [(64, 40), (768, 768), (768, 1001), (2048, 768), (4096, 264),
+                                 (682, 256), (1365, 512), (7, 9)])
 @pytest.mark.parametrize("epilogue", ["store", "add", "swiglu"])
 def test_rows_linear_matches_torch(M, K, N, epilogue):
     g = torch.Generator().manual_seed(M * 7 + K + N)

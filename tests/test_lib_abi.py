@@ -227,11 +227,12 @@ def test_rows_linear_argument_checks():
 
     assert lin(M=9) == -2 and "rows" in _err()
     assert lin(M=-1) == -2
-    assert lin(K=12, xs=16) == -2 and "multiple of 8" in _err()
+    assert lin(K=0, xs=16) == -2 and "outside" in _err()
     assert lin(K=4104, xs=4104) == -2
     assert lin(N=0) == -1
     assert lin(x=None) == -1 and "NULL" in _err()
-    assert lin(x=ctypes.c_void_p(0x1008)) == -1 and "aligned" in _err()
+    assert lin(x=ctypes.c_void_p(0x1001)) == -1 and "aligned" in _err()
+    assert lin(nw=ctypes.c_void_p(0x1002), ndt=1) == -1 and "misaligned" in _err()
     assert lin(xs=760) == -1 and "stride" in _err()
     assert lin(nw=P, ndt=2) == -2 and "dtype" in _err()
     assert lin(ep=3) == -2 and "epilogue" in _err()
