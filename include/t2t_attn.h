@@ -352,8 +352,10 @@ int t2t_rows_qkv_rope(const void *x, int64_t x_stride, int32_t M, int32_t K, con
  * reference, which recomputes every position per token: generation_loop.py:90-92).
  *   tokens_*  int64[n], doc_* int32[n], q_bits_* / kv_bits_* uint64
  *             [words][bits_stride_*] (bits_stride >= n; NULL when words == 0).
- *   out       int32[1] (device), written with the result.
- * One work-group; 0 <= words <= T2T_MAX_WORDS.
+ *   out       int32[1] (device): must hold n (or any value >= n) when the call
+ *             runs (e.g. a fill on the same stream); the call lowers it to the
+ *             first differing position with an atomic min, so it ends as the
+ *             result.  0 <= words <= T2T_MAX_WORDS.
  */
 int t2t_first_input_diff(const int64_t *tokens_a, const int64_t *tokens_b, const int32_t *doc_a,
                          const int32_t *doc_b, const uint64_t *q_bits_a, const uint64_t *q_bits_b,

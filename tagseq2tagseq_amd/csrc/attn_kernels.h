@@ -146,8 +146,8 @@ hipError_t launch_rows_qkv_rope(const __bf16* x, int64_t xs, int M, int K, const
                                 int max_pos, const TensorView& q, const TensorView& k,
                                 const TensorView& v, hipStream_t stream);
 
-// First position < n at which two copies of per-token inputs differ, or n
-// (one work-group; bits arrays [words][stride]).
+// First position < n at which two copies of per-token inputs differ: lowers
+// *out (preset to n by the caller) to it (bits arrays [words][stride]).
 hipError_t launch_first_input_diff(const int64_t* ta, const int64_t* tb, const int32_t* da,
                                    const int32_t* db, const uint64_t* qa, const uint64_t* qb,
                                    const uint64_t* ka, const uint64_t* kb, int64_t sa, int64_t sb,

@@ -60,8 +60,8 @@ class KVCache:
     def first_diff(self, tokens: torch.Tensor, bm, n: int) -> torch.Tensor:
         """Device int32 [1]: the first of positions 0 .. n - 1 whose token id
         or mask inputs (doc id, q / kv words) differ from the cached ones, or n
-        (``t2t_first_input_diff``, one launch, no host sync)."""
-        out = torch.empty(1, dtype=torch.int32, device=self.tokens.device)
+        (``t2t_first_input_diff`` lowering a fill of n; no host sync)."""
+        out = torch.full((1,), n, dtype=torch.int32, device=self.tokens.device)
 
         def row(t):
             t = t[0]
