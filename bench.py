@@ -114,10 +114,33 @@ def time_launches(fn, reps: int) -> float:
     return start.elapsed_time(end) / reps
 
 
-def cpu_baseline(rows_np, c, seed, threads):
-    """Reference CPU path on one head: create_block_mask + eager flex_attention
-    fwd+bwd (torch/_higher_order_ops/flex_attention.py:202-294, 825-994) with the
-    reference's mask_mod (restated in oracle/mask_oracle.py)."""
+def host_cores():
+    """(CPUs this process may run on, CPUs the host reports)."""
+    try:
+        avail = len(os.sched_getaffinity(0))
+    except AttributeError:
+        avail = os.cpu_count() or 1
+    return avail, os.cpu_count() or avail
+
+
+def _median_spread(fn, reps: int):
+    """One untimed warm-up call, then `reps` timed calls: (median, min, max) s."""
+    fn()
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    ts.sort()
+    return ts[len(ts) // 2], ts[0], ts[-1]
+
+
+def cpu_baseline(rows_np, c, seed, threads, reps=5):
+    """Reference CPU path on one head of batch row 0, each phase timed on its
+    own (one warm-up, median of `reps`): create_block_mask with the reference's
+    mask_mod (restated in oracle/mask_oracle.py), eager flex_attention forward,
+    and forward + backward (torch/_higher_order_ops/flex_attention.py:202-294,
+    825-994).  Returns the per-phase statistics and the scaled step time."""
     from oracle.mask_oracle import torch_mask_mod
     from torch.nn.attention.flex_attention import create_block_mask, flex_attention
     torch.set_num_threads(threads)
@@ -126,23 +149,30 @@ def cpu_baseline(rows_np, c, seed, threads):
     mod = torch_mask_mod(torch.from_numpy(doc),
                          None if qb is None else torch.from_numpy(qb.view(np.int64)),
                          None if kb is None else torch.from_numpy(kb.view(np.int64)))
-    t0 = time.perf_counter()
     bm = create_block_mask(mod, None, None, T, T, device="cpu")
-    t_mask = time.perf_counter() - t0
     g = torch.Generator().manual_seed(seed)
     dt = torch.bfloat16
     q = torch.randn(1, 1, T, D, generator=g).to(dt).requires_grad_(True)
     k = torch.randn(1, 1, T, D, generator=g).to(dt).requires_grad_(True)
     v = torch.randn(1, 1, T, D, generator=g).to(dt).requires_grad_(True)
     do = torch.randn(1, 1, T, D, generator=g).to(dt)
-    t0 = time.perf_counter()
-    out = flex_attention(q, k, v, block_mask=bm)
-    out.backward(do)
-    t_head = time.perf_counter() - t0
-    n_rows = len(rows_np)
+
+    def fwd():
+        with torch.no_grad():
+            flex_attention(q, k, v, block_mask=bm)
+
+    def fwd_bwd():
+        q.grad = k.grad = v.grad = None
+        flex_attention(q, k, v, block_mask=bm).backward(do)
+
+    phases = {
+        "mask": _median_spread(lambda: create_block_mask(mod, None, None, T, T, device="cpu"), reps),
+        "fwd_head": _median_spread(fwd, reps),
+        "fwd_bwd_head": _median_spread(fwd_bwd, reps),
+    }
     # Cost is linear in heads and in independent batch rows.
-    t_step = n_rows * (t_mask + c["Hq"] * t_head)
-    return t_step, t_mask, t_head
+    t_step = len(rows_np) * (phases["mask"][0] + c["Hq"] * phases["fwd_bwd_head"][0])
+    return t_step, phases
 
 
 def prologue_stats(dev, T: int, C: int, H: int, reps: int):
@@ -271,7 +301,10 @@ def decode_bench(args, dev):
         the reference's per-token path (model/generation_loop.py:90-92), 3 steps;
       * the decode attention kernel alone at one layer's shape (Tq 1, H 12,
         D 64, all context keys): algorithmic bytes = allowed keys x H x 4 D
-        (K and V rows) + H x Tkv x (4 + 8 W) (mask inputs read per head)."""
+        (K and V rows) + H x Tkv x (4 + 8 W) (mask inputs read per head).
+    With --no-graphs nothing is captured as a HIP graph: the steps run eagerly
+    and the kernel loop launches directly (the form for rocprofv3 counter
+    passes, which serialise and instrument every dispatch)."""
     import numpy as np
     from tagseq2tagseq_amd.decode import attn_decode
     from tagseq2tagseq_amd.mask_creators import create_doc_link_block_mask
@@ -296,6 +329,8 @@ def decode_bench(args, dev):
         sp[-1] = synth.DocSpan(doc_id=last.doc_id, start=last.start, end=T0 + n)
         return stream[:, :T0 + n], sp
 
+    graphs = not args.no_graphs
+    model.use_graphs = graphs
     tok, sp = grown(0)
     model.forward_inference_last(tok, sp, doc_links=links)  # prefill
     n_steps = min(args.steps, 60 - args.warmup)
@@ -316,9 +351,11 @@ def decode_bench(args, dev):
         tok, sp = grown(i)
         model.forward_inference_last(tok, sp, doc_links=links).argmax().item()
     eager_ms = 1e3 * (time.perf_counter() - t0) / n_steps
-    model.use_graphs = True
+    model.use_graphs = graphs
 
     def replay_us(reps=50):
+        if not graphs:
+            return None
         # GPU time of one captured step (the graph alone, no host work)
         g = model._graph.graph
         g.replay()
@@ -380,17 +417,23 @@ def decode_bench(args, dev):
     # one ctypes call with two dozen arguments: the calls are captured into a
     # HIP graph on a side stream and the replays are timed, so the figure is
     # the kernels' time, not the host's.
-    side = torch.cuda.Stream(dev)
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph, stream=side):
-        cap_args = call_args[:-1] + (ctypes.c_void_p(side.cuda_stream),)
-        for _ in range(args.reps):
-            _lib.check(L.t2t_attn_decode(*cap_args), "t2t_attn_decode")
-    graph.replay()
+    if graphs:
+        side = torch.cuda.Stream(dev)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=side):
+            cap_args = call_args[:-1] + (ctypes.c_void_p(side.cuda_stream),)
+            for _ in range(args.reps):
+                _lib.check(L.t2t_attn_decode(*cap_args), "t2t_attn_decode")
+        run_reps = graph.replay
+    else:
+        def run_reps():
+            for _ in range(args.reps):
+                L.t2t_attn_decode(*call_args)
+    run_reps()
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
-    graph.replay()
+    run_reps()
     e1.record()
     torch.cuda.synchronize()
     k_us = 1e3 * e0.elapsed_time(e1) / args.reps
@@ -409,8 +452,10 @@ def decode_bench(args, dev):
         "data": "synthetic (random token ids, seeded packed documents, random-init weights)",
         "config": {"workload": "decode steps on the configs[4] model", "context": T0,
                    "vocab": V, "n_docs": len(spans), "grant_words": W},
-        "graph_step_gpu_us": round(step_us, 1),
-        "graph_step_gpu_us_unfused_layers": round(unfused_step_us, 1),
+        "graph_step_gpu_us": None if step_us is None else round(step_us, 1),
+        "graph_step_gpu_us_unfused_layers": (None if unfused_step_us is None
+                                             else round(unfused_step_us, 1)),
+        "graphs": graphs,
         "eager_cached_ms_per_token": round(eager_ms, 3),
         "full_recompute_ms_per_token": round(full_ms, 2),
         "speedup_vs_full_recompute": round(full_ms / cached_ms, 1),
@@ -549,30 +594,37 @@ def config1_bench(args, dev):
     if not args.no_cpu_baseline:
         torch.set_num_threads(args.cpu_threads)
         mod = torch_mask_mod(torch.from_numpy(rows_np[0][0]), None, None)
-        t0 = time.perf_counter()
-        cbm = create_block_mask(mod, None, None, T, T, device="cpu")
-        out = torch_flex(qc, kc, vc, block_mask=cbm)
-        t_eager = time.perf_counter() - t0
+
+        def cpu_step():
+            m = create_block_mask(mod, None, None, T, T, device="cpu")
+            return m, torch_flex(qc, kc, vc, block_mask=m)
+
+        t_eager, t_lo, t_hi = _median_spread(cpu_step, args.cpu_reps)
+        cbm, out = cpu_step()
         # same inputs: the GPU float32 forward against the reference's CPU output
         got = attn_fwd(q, k, v, bm, scale)[0].float().cpu()
         max_err = float((got - out).abs().max())
+        avail, reported = host_cores()
         result["cpu_baseline"] = {
             "value": round(useful / t_eager / 1e12, 6), "unit": "TFLOP/s",
-            "cores": args.cpu_threads, "kind": "reference",
+            "cores": args.cpu_threads, "host_cpus": {"os_cpu_count": reported, "affinity": avail},
+            "kind": "reference", "reps": args.cpu_reps,
+            "phases_s": {"mask+fwd": {"median": round(t_eager, 4), "min": round(t_lo, 4),
+                                      "max": round(t_hi, 4)}},
             "sample": (f"torch {torch.__version__} eager create_block_mask + flex_attention "
-                       f"forward, float32, all {Hq} heads, on CPU ({t_eager:.3f} s)"),
+                       f"forward, float32, all {Hq} heads, on CPU (median of {args.cpu_reps} after "
+                       f"1 warm-up: {t_eager:.3f} s)"),
             "max_abs_diff_vs_gpu": max_err,
         }
         try:
             cf = torch.compile(torch_flex)
             cf(qc, kc, vc, block_mask=cbm)  # compile
-            t0 = time.perf_counter()
-            cf(qc, kc, vc, block_mask=cbm)
-            t_comp = time.perf_counter() - t0
+            t_comp, _, _ = _median_spread(lambda: cf(qc, kc, vc, block_mask=cbm), args.cpu_reps)
             result["cpu_compiled_fwd"] = {"s": round(t_comp, 4),
                                           "TFLOPs": round(useful / t_comp / 1e12, 6),
                                           "sample": "torch.compile(flex_attention) forward on CPU, "
-                                                    "block mask prebuilt, second call"}
+                                                    f"block mask prebuilt, median of {args.cpu_reps} "
+                                                    "after the compiling call and 1 warm-up"}
         except Exception as e:  # inductor's CPU path needs a host C++ toolchain
             result["cpu_compiled_fwd"] = {"error": f"{type(e).__name__}: {str(e)[:200]}"}
     print(json.dumps(result))
@@ -647,7 +699,10 @@ def main():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--reps", type=int, default=20, help="launches per per-kernel timing")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-threads", type=int, default=min(16, os.cpu_count() or 1))
+    ap.add_argument("--cpu-threads", type=int, default=host_cores()[0],
+                    help="CPU-baseline threads (default: every CPU this process may use)")
+    ap.add_argument("--cpu-reps", type=int, default=5,
+                    help="timed repetitions per CPU-baseline phase (after one warm-up)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device copy (HBM-counter calibration)")
     ap.add_argument("--schedule", action="store_true",
@@ -656,6 +711,9 @@ def main():
     ap.add_argument("--decode", action="store_true",
                     help="generation with the key/value cache on the configs[4] model "
                          "(per-token latency, cached vs full recompute, decode kernel roofline)")
+    ap.add_argument("--no-graphs", action="store_true",
+                    help="with --decode: run every step eagerly and launch the kernel loop "
+                         "directly, capturing no HIP graph")
     ap.add_argument("--rows", action="store_true",
                     help="the fused few-row linear kernels of a decode step, each timed alone")
     ap.add_argument("--rows-eager", action="store_true",
@@ -850,16 +908,22 @@ def main():
     }
 
     if not args.no_cpu_baseline:
-        t_step, t_mask, t_head = cpu_baseline(rows_np, c, args.seed, args.cpu_threads)
+        t_step, ph_cpu = cpu_baseline(rows_np, c, args.seed, args.cpu_threads, args.cpu_reps)
+        avail, reported = host_cores()
         result["cpu_baseline"] = {
             "value": round(useful_flops / t_step / 1e12, 6),
             "unit": "TFLOP/s",
             "cores": args.cpu_threads,
+            "host_cpus": {"os_cpu_count": reported, "affinity": avail},
             "kind": "reference",
-            "sample": (f"torch {torch.__version__} eager create_block_mask + flex_attention fwd+bwd "
-                       f"on CPU with the reference mask_mod, 1 of {Hq} heads of batch row 0 "
-                       f"(mask {t_mask:.2f} s, head {t_head:.2f} s), scaled x{Hq} heads "
-                       f"x{len(rows_np)} rows"),
+            "reps": args.cpu_reps,
+            "phases_s": {n: {"median": round(m, 4), "min": round(lo, 4), "max": round(hi, 4)}
+                         for n, (m, lo, hi) in ph_cpu.items()},
+            "sample": (f"torch {torch.__version__} on CPU, reference mask_mod: create_block_mask, "
+                       f"eager flex_attention fwd and fwd+bwd on 1 of {Hq} heads of batch row 0, "
+                       f"median of {args.cpu_reps} after 1 warm-up each; step = rows x (mask + "
+                       f"{Hq} x fwd+bwd head) = {len(rows_np)} x ({ph_cpu['mask'][0]:.2f} + {Hq} x "
+                       f"{ph_cpu['fwd_bwd_head'][0]:.2f}) s"),
             "s_per_step": round(t_step, 2),
         }
     print(json.dumps(result))

@@ -26,6 +26,7 @@ from __future__ import annotations
 
 import ctypes
 import math
+import warnings
 from typing import Optional
 
 import torch
@@ -317,7 +318,8 @@ class FlexSelfAttention(nn.Module):
     projection reads it without a transpose copy.  The reference's module
     comes from the absent ``tunalab`` package; its internal details (RoPE
     variant, QK-norm, fp8 out-projection) are not available here, so
-    ``fp8_out_proj`` is accepted and ignored.
+    ``fp8_out_proj=True`` is accepted for signature compatibility, warned
+    about once, and the output projection stays in the module's dtype.
     """
 
     def __init__(self, dim: int, num_heads: int, max_seq_len: int, fp8_out_proj: bool = False):
@@ -331,6 +333,9 @@ class FlexSelfAttention(nn.Module):
         self.proj = nn.Linear(dim, dim, bias=False)
         self.rotary = Rotary(self.head_dim, max_seq_len)
         self.fp8_out_proj = fp8_out_proj
+        if fp8_out_proj:
+            warnings.warn("FlexSelfAttention(fp8_out_proj=True): the fp8 output projection is not "
+                          "implemented; the projection runs in the module's dtype", stacklevel=2)
 
     def forward(self, x: torch.Tensor, block_mask: T2TBlockMask) -> torch.Tensor:
         from .rope import qkv_rope

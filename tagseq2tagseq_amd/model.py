@@ -15,7 +15,12 @@ position whose inputs are unchanged since the previous call (``KVCache``).
 The reusable prefix is the longest one over which the token ids and all mask
 inputs (doc id, q words, kv words) agree: a position's hidden states depend
 only on the positions before it and on its own mask row, so they are exact
-for that prefix.  New rows go through each layer with the decode-step kernel
+for that prefix.  The cache also records the weights it was filled with --
+each parameter's storage address and version counter, and the train / eval
+mode -- and is dropped when any of them changes (an optimizer step,
+load_state_dict, an in-place edit, train() / eval()).  Writes through a
+parameter's ``.data`` bypass its version counter; call ``reset_cache()`` after
+such an edit.  New rows go through each layer with the decode-step kernel
 (``t2t_attn_decode``, up to 8 rows per kv head per launch); when more than
 ``prefill_rows`` rows are new, the whole sequence is recomputed through the
 block-mask kernels and the cache refilled.
@@ -119,6 +124,7 @@ class TS2TSModel:
         self.use_graphs = True
         self.fuse_rows = True  # few-row steps on the fused row kernels (rows.py)
         self._graph: Optional[_DecodeGraph] = None
+        self._weights_seen = None  # _weights_state() the cache was filled under
 
     @classmethod
     def from_config(cls, vocab_size: int, num_layers: int, model_dim: int, num_heads: int,
@@ -161,6 +167,16 @@ class TS2TSModel:
     def reset_cache(self) -> None:
         self.kv_cache = None
         self._graph = None
+        self._weights_seen = None
+
+    def _weights_state(self):
+        """What the cached keys / values depend on besides the inputs: the mode
+        and, per parameter, its storage address and version counter (bumped by
+        every in-place write through the parameter, optimizer steps and
+        load_state_dict included)."""
+        params = (*self.backbone.parameters(), *self.norm.parameters(), self.embedding_weight,
+                  self.lm_head_weight)
+        return self.backbone.training, tuple((p.data_ptr(), p._version) for p in params)
 
     @torch.no_grad()
     def forward_inference(self, tokens: torch.Tensor, doc_spans: Optional[List[Any]] = None,
@@ -199,6 +215,10 @@ class TS2TSModel:
         bm = self.block_mask_creator(tokens=tokens, doc_spans=doc_spans or [], inputs_only=True,
                                      **kwargs)
         T = tokens.shape[1]
+        state = self._weights_state()
+        if state != self._weights_seen:
+            self.reset_cache()
+            self._weights_seen = state
         cache = self.kv_cache
         if cache is None or cache.words != bm.words or T > cache.capacity:
             cache = self.kv_cache = self._new_cache(bm.words, tokens.device)

@@ -119,15 +119,26 @@ def test_too_many_rows_raises():
 
 # -- cached model path ------------------------------------------------------
 
-def _model(creator, T_max=1024):
+def _distinct_skip_weights(m):
+    """Skip weights 0.5, 1.5, 0.75, ... instead of the all-ones init, so that a
+    skip add that takes the wrong weight or the wrong popped row changes the
+    logits (model/modules/backbone.py:93-104)."""
+    vals = [0.5, 1.5, 0.75, 1.25, 0.625, 1.375]
+    with torch.no_grad():
+        sw = m.backbone.skip_weights
+        sw.copy_(torch.tensor(vals[:sw.numel()], dtype=sw.dtype))
+
+
+def _model(creator, T_max=1024, num_layers=4):
     # model_dim 384: GLU hidden width 1024, a multiple of 8, so the row
     # kernels read every operand in 16-byte vectors
     torch.manual_seed(0)
-    m = TS2TSModel.from_config(vocab_size=500, num_layers=4, model_dim=384, num_heads=6,
+    m = TS2TSModel.from_config(vocab_size=500, num_layers=num_layers, model_dim=384, num_heads=6,
                                max_seq_len=T_max, dropout=0.0, drop_path_rate=0.0,
                                block_mask_creator=creator)
     with torch.no_grad():
         m.embedding_weight.mul_(0.05)  # keeps logits in a range where bf16 rounding is small
+    _distinct_skip_weights(m)
     return m.to(DEV, torch.bfloat16).eval()
 
 
@@ -145,11 +156,12 @@ def _grow(spans, n):
     return spans[:-1] + [synth.DocSpan(doc_id=last.doc_id, start=last.start, end=last.end + n)]
 
 
-@pytest.mark.parametrize("graphs", [True, False])
-def test_cached_generation_matches_full_recompute(graphs):
+@pytest.mark.parametrize("graphs,layers", [(True, 4), (False, 4), (True, 5)])
+def test_cached_generation_matches_full_recompute(graphs, layers):
     """Single-row steps run through the captured HIP graph (graphs=True, replayed
-    with eager work and host synchronisation between replays) or eagerly."""
-    m = _model(create_doc_causal_block_mask)
+    with eager work and host synchronisation between replays) or eagerly; five
+    layers leave the last layer with no skip row to pop."""
+    m = _model(create_doc_causal_block_mask, num_layers=layers)
     m.use_graphs = graphs
     g = torch.Generator().manual_seed(1)
     vocab = torch.randint(0, 500, (1, 1024), generator=g).to(DEV)
@@ -234,8 +246,8 @@ def test_cached_generation_cross_doc_links(graphs):
 
 
 @pytest.mark.parametrize("graphs", [True, False])
-@pytest.mark.parametrize("dim,heads", [(384, 6), (256, 4)])
-def test_fused_row_kernels_match_unfused_layers(graphs, dim, heads, monkeypatch):
+@pytest.mark.parametrize("dim,heads,layers", [(384, 6, 4), (256, 4, 4), (384, 6, 5)])
+def test_fused_row_kernels_match_unfused_layers(graphs, dim, heads, layers, monkeypatch):
     """Decode steps on the fused row kernels (norm + qkv + rotation + cache
     write, out-projection + residual, norm + gate_up + SwiGLU, down +
     residual, norm + LM head) against the same steps through the unfused torch
@@ -248,11 +260,12 @@ def test_fused_row_kernels_match_unfused_layers(graphs, dim, heads, monkeypatch)
     monkeypatch.setattr(model_mod, "rows_linear",
                         lambda *a, **kw: calls.append(1) or real(*a, **kw))
     torch.manual_seed(0)
-    m = TS2TSModel.from_config(vocab_size=500, num_layers=4, model_dim=dim, num_heads=heads,
+    m = TS2TSModel.from_config(vocab_size=500, num_layers=layers, model_dim=dim, num_heads=heads,
                                max_seq_len=1024, dropout=0.0, drop_path_rate=0.0,
                                block_mask_creator=create_doc_causal_block_mask)
     with torch.no_grad():
         m.embedding_weight.mul_(0.05)
+    _distinct_skip_weights(m)
     m = m.to(DEV, torch.bfloat16).eval()
     m.use_graphs = graphs
     g = torch.Generator().manual_seed(3)
@@ -273,6 +286,43 @@ def test_fused_row_kernels_match_unfused_layers(graphs, dim, heads, monkeypatch)
         err = (fused - plain).abs().max().item()
         assert err <= 2e-2 * scale + 1e-3, f"{n} rows: max err {err:.4g} (scale {scale:.3g})"
     assert calls, "the fused row kernels did not run"
+
+
+@pytest.mark.parametrize("graphs", [True, False])
+def test_cache_dropped_when_weights_change(graphs):
+    """The cached keys / values and the captured step are rebuilt after an
+    in-place weight edit, load_state_dict, an optimizer step and a train() /
+    eval() switch: each following call equals the full recompute under the
+    new weights (the reference recomputes every call, model/model.py:214-237)."""
+    m = _model(create_doc_causal_block_mask)
+    m.use_graphs = graphs
+    g = torch.Generator().manual_seed(4)
+    vocab = torch.randint(0, 500, (1, 1024), generator=g).to(DEV)
+    spans = [synth.DocSpan(doc_id=2, start=0, end=250)]
+    T = 250
+    _check_last(m, vocab[:, :T], spans, "prefill")
+
+    def step(what):
+        nonlocal spans, T
+        spans = _grow(spans, 1)
+        T += 1
+        _check_last(m, vocab[:, :T], spans, what)
+
+    step("decode")  # the single-row step exists now (captured when graphs=True)
+    with torch.no_grad():
+        m.backbone.layers[1].attn.qkv.weight.mul_(1.5)
+    step("after an in-place edit")
+    sd = {k: v * 0.9 for k, v in m.backbone.state_dict().items()}
+    m.backbone.load_state_dict(sd)
+    step("after load_state_dict")
+    opt = torch.optim.SGD(m.backbone.parameters(), lr=1.0)
+    for p_ in m.backbone.parameters():
+        p_.grad = torch.full_like(p_, 1e-3)
+    opt.step()
+    step("after an optimizer step")
+    m.train()
+    m.eval()
+    step("after train() / eval()")
 
 
 @pytest.mark.parametrize("words", [0, 1, 3])

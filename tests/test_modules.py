@@ -113,3 +113,36 @@ def test_token_lists_packing_clips_bounds_and_wraps_doc_ids():
         cnt = np.array([[len(r) for r in spans], [len(r) for r in grants]])
         ref = np.concatenate([sp.ravel(), gr.ravel(), cnt.ravel()]).astype(np.int32)
         assert np.array_equal(got, ref)
+
+
+def test_fp8_out_proj_is_warned_about():
+    import warnings
+    from tagseq2tagseq_amd.attention import FlexSelfAttention
+    with warnings.catch_warnings(record=True) as w:
+        warnings.simplefilter("always")
+        FlexSelfAttention(64, 2, 128)
+        assert not w
+        m = FlexSelfAttention(64, 2, 128, fp8_out_proj=True)
+    assert m.fp8_out_proj and any("fp8" in str(x.message) for x in w)
+
+
+def test_model_weights_state_tracks_edits_and_mode():
+    """TS2TSModel drops its generation cache when this state changes."""
+    from tagseq2tagseq_amd.model import TS2TSModel
+    torch.manual_seed(0)
+    m = TS2TSModel.from_config(vocab_size=50, num_layers=2, model_dim=64, num_heads=2,
+                               max_seq_len=64, dropout=0.0, drop_path_rate=0.0,
+                               block_mask_creator=None).eval()
+    s0 = m._weights_state()
+    assert m._weights_state() == s0
+    with torch.no_grad():
+        m.backbone.layers[0].mlp.down.weight.add_(1.0)
+    s1 = m._weights_state()
+    assert s1 != s0
+    m.backbone.load_state_dict(m.backbone.state_dict())
+    s2 = m._weights_state()
+    assert s2 != s1
+    m.train()
+    assert m._weights_state() != s2
+    m.eval()
+    assert m._weights_state() == s2

@@ -215,6 +215,21 @@ def test_link_matching_dag_rule():
     assert c._match_links_to_docs(links, spans) == {15: [7]}
 
 
+def test_document_ids_known_answer():
+    """Explicit expected maps (block_mask_creator.py:107-117 semantics): doc 5
+    on [-3, 4) is clipped at 0; doc 7 on [8, 40) is clipped at T = 20 and
+    overwrites token 8 of doc 6; doc 9 on [12, 14) overwrites the middle of
+    doc 7; doc 2 on [30, 35) lies past T and writes nothing.  The second case
+    leaves gaps, which stay -1."""
+    spans = _spans((5, -3, 4), (6, 4, 9), (7, 8, 40), (9, 12, 14), (2, 30, 35))
+    want = np.array([5, 5, 5, 5, 6, 6, 6, 6, 7, 7, 7, 7, 9, 9, 7, 7, 7, 7, 7, 7], np.int32)
+    assert np.array_equal(mo.document_ids(20, spans), want)
+    gap = _spans((1, 0, 3), (2, 5, 7))  # tokens 3, 4 and 7.. uncovered: -1
+    want_gap = np.array([1, 1, 1, -1, -1, 2, 2, -1, -1], np.int32)
+    assert np.array_equal(mo.document_ids(9, gap), want_gap)
+    assert np.array_equal(document_ids_host(9, gap), want_gap)
+
+
 def test_document_ids_host_matches_oracle():
     spans = _spans((5, -3, 4), (6, 4, 9), (7, 8, 40))  # clipped, overlapping, overflow
     assert np.array_equal(document_ids_host(20, spans), mo.document_ids(20, spans))
