@@ -53,8 +53,9 @@ def test_config5_training_steps():
         opt.step()
         opt.zero_grad(set_to_none=True)
         losses.append(float(loss.detach()))
+    # (nn.Embedding's N(0, 1) init tied to the head, as in the reference's
+    # from_config, training_module.py:120, puts the first loss far above ln V)
     assert all(math.isfinite(x) for x in losses), losses
-    assert abs(losses[0] - math.log(VOCAB)) < 1.0, f"random-init loss {losses[0]:.3f}"
     assert losses[2] < losses[1] < losses[0], losses
 
 
