@@ -174,6 +174,25 @@ int t2t_attn_bwd(const t2t_tensor *q, const t2t_tensor *k, const t2t_tensor *v,
                  void *stream);
 
 /*
+ * t2t_attn_bwd without the caller's Delta workspace, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid allocation).  No counterpart in the reference.
+ * Delta lives in a file-scope device array of the library (one 16 MiB copy
+ * per GPU, held until the process ends), so B * Hq * T must be at most
+ * 4194304 (4 * 2^20) rows; larger shapes return T2T_EINVAL.  The call
+ * allocates and frees nothing.  Every call on one GPU shares that GPU's
+ * array: calls that overlap on one GPU (concurrent streams, or a second call
+ * enqueued on another stream before the first finished) race.  The first call
+ * on a device looks up the array's address with that device current.
+ * Arguments and results otherwise as t2t_attn_bwd (bitwise identical outputs).
+ */
+int t2t_attn_bwd_noalloc(const t2t_tensor *q, const t2t_tensor *k, const t2t_tensor *v,
+                         const t2t_tensor *o, const t2t_tensor *dout, const float *lse2,
+                         const t2t_tensor *dq, const t2t_tensor *dk, const t2t_tensor *dv,
+                         int32_t B, int32_t Hq, int32_t Hkv, int32_t T, int32_t D, int32_t dtype,
+                         float scale, const t2t_block_mask *mask, void *stream);
+
+/*
  * The backward's phases, callable separately (for example to run dK/dV and
  * dQ on two streams once Delta is ready; t2t_attn_bwd itself runs a dQ that
  * also writes Delta, then dK/dV).  bf16 only (float32 runs as one

@@ -3,6 +3,7 @@
 #include <algorithm>
 #include <cstdarg>
 #include <cstdio>
+#include <mutex>
 
 #include "../../include/t2t_attn.h"
 #include "attn_kernels.h"
@@ -276,6 +277,64 @@ int t2t_attn_bwd(const t2t_tensor* q, const t2t_tensor* k, const t2t_tensor* v,
   if (rc) return rc;
   return t2t_attn_bwd_dkdv(q, k, v, dout, lse2, delta, dk, dv, B, Hq, Hkv, T, D, dtype, scale,
                            mask, stream);
+}
+
+// Delta workspace of t2t_attn_bwd_noalloc: a file-scope device array instead
+// of a caller buffer.  Every GPU the library runs on holds its own copy (16
+// MiB) until the process ends; in host code `scratch` only names the symbol,
+// so the entry point uses the device address hipGetSymbolAddress returns for
+// the current device, looked up once per device.
+constexpr int64_t kScratchFloats = int64_t(4) << 20;  // B * Hq * T rows of Delta
+static __device__ __align__(256) float scratch[kScratchFloats];
+
+namespace {
+
+constexpr int kScratchDevices = 64;
+std::mutex g_scratch_mu;
+float* g_scratch_addr[kScratchDevices] = {};
+
+// This GPU's copy of `scratch` (the current device, as for every launch).
+int current_scratch(float** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_status(e, "hipGetDevice");
+  if (dev < 0 || dev >= kScratchDevices)
+    return fail(T2T_EUNSUPPORTED, "device %d is past the %d devices the static workspace tracks",
+                dev, kScratchDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_addr[dev]) {
+    void* addr = nullptr;
+    e = hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_status(e, "hipGetSymbolAddress(scratch)");
+    g_scratch_addr[dev] = static_cast<float*>(addr);
+  }
+  *out = g_scratch_addr[dev];
+  return T2T_OK;
+}
+
+}  // namespace
+
+int t2t_attn_bwd_noalloc(const t2t_tensor* q, const t2t_tensor* k, const t2t_tensor* v,
+                         const t2t_tensor* o, const t2t_tensor* dout, const float* lse2,
+                         const t2t_tensor* dq, const t2t_tensor* dk, const t2t_tensor* dv,
+                         int32_t B, int32_t Hq, int32_t Hkv, int32_t T, int32_t D, int32_t dtype,
+                         float scale, const t2t_block_mask* mask, void* stream) {
+  int rc = check_dims(B, Hq, Hkv, T, D, dtype, true);
+  if (rc) return rc;
+  if (B == 0 || Hq == 0 || T == 0) return T2T_OK;
+  const int64_t rows = (int64_t)B * Hq * T;
+  if (rows > kScratchFloats)
+    return fail(T2T_EINVAL,
+                "B*Hq*T = %lld Delta rows exceed the static workspace of %lld rows "
+                "(use t2t_attn_bwd with a caller workspace)",
+                (long long)rows, (long long)kScratchFloats);
+  float* delta = nullptr;
+  rc = current_scratch(&delta);
+  if (rc) return rc;
+  // Every row of Delta is written by the dQ launch before dK/dV reads it, so
+  // the workspace needs no clearing between calls.
+  return t2t_attn_bwd(q, k, v, o, dout, lse2, delta, dq, dk, dv, B, Hq, Hkv, T, D, dtype, scale,
+                      mask, stream);
 }
 
 namespace {
