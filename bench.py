@@ -100,6 +100,17 @@ def measured_traffic(config: int, kernel: str):
     return None
 
 
+def profile_mfma_busy(config: int):
+    """MFMA-busy fraction per kernel from the committed instruction-mix summary
+    (profiles/instruction_mix_config<N>.txt: SQ_VALU_MFMA_BUSY_CYCLES over the
+    chip's SIMD-cycles in the kernel's duration, from rocprofv3 runs of this
+    bench), or None when no summary exists."""
+    from tagseq2tagseq_amd.rocprof_summary import read_mfma_busy
+    path = os.path.join(ROOT, "profiles", f"instruction_mix_config{config}.txt")
+    got = read_mfma_busy(path)
+    return {"source": os.path.relpath(path, ROOT), **got} if got else None
+
+
 def time_launches(fn, reps: int) -> float:
     """Mean duration (ms) of fn()'s launches, HIP events on the current stream."""
     start = torch.cuda.Event(enable_timing=True)
@@ -889,6 +900,7 @@ def main():
             "traffic": measured_traffic(args.config, dom),
             "traffic_source": f"profiles/hbm_traffic_config{args.config}.txt",
         },
+        "mfma_busy": profile_mfma_busy(args.config),
         "kernels_ms": {
             "token_inputs_kernel": round(t_tok, 4),
             "mask_meta (3 launches)": round(t_meta, 4),

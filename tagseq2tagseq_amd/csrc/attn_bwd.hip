@@ -81,18 +81,31 @@ __global__ __launch_bounds__(kThreads) void bwd_delta_kernel(BwdParams p) {
 
 // P and dS of a mixed dK/dV block in place (sacc -> P, dpacc -> dS) for a
 // lane whose bitmap word, shifted right by its lane group, is wg: P of a
-// masked pair is cleared with the pair's sign-extended mask bit.
+// masked pair is cleared with the pair's sign-extended mask bit.  l / d: the
+// lane's 16 rows' LSE and Delta in accumulator order.
 template <int I = 0>
-__device__ __forceinline__ void keep_masked(f32x16& sacc, uint32_t wg, const float* lu,
-                                            const float* dlu, f32x16& dpacc, float c, int g) {
+__device__ __forceinline__ void keep_masked(f32x16& sacc, uint32_t wg, const f32x16& l,
+                                            const f32x16& d, f32x16& dpacc, float c) {
   if constexpr (I < 16) {
-    const int qr = acc_row(I, g);
-    const float e = fast_exp2(fmaf(sacc[I], c, -lu[qr]));
+    const float e = fast_exp2(fmaf(sacc[I], c, -l[I]));
     const float pv = __int_as_float(__float_as_int(e) & sbfe1_c<acc_tok_bit(I)>(wg));
     sacc[I] = pv;
-    dpacc[I] = pv * (dpacc[I] - dlu[qr]);
-    keep_masked<I + 1>(sacc, wg, lu, dlu, dpacc, c, g);
+    dpacc[I] = pv * (dpacc[I] - d[I]);
+    keep_masked<I + 1>(sacc, wg, l, d, dpacc, c);
   }
+}
+
+// The 16 accumulator rows of lane group g (rows 8 a + 4 g + 0..3) of a
+// 32-row slot array, as four 16-byte reads -- the same reads for mixed and
+// unmasked blocks.
+__device__ __forceinline__ f32x16 acc_rows(const float* base, int g) {
+  f32x16 r;
+#pragma unroll
+  for (int a = 0; a < 4; ++a) {
+    const float4 x = *reinterpret_cast<const float4*>(base + 8 * a + 4 * g);
+    r[4 * a] = x.x; r[4 * a + 1] = x.y; r[4 * a + 2] = x.z; r[4 * a + 3] = x.w;
+  }
+  return r;
 }
 
 constexpr int kDkdvWaves = 8;  // 4 key groups x 2 query blocks
@@ -122,7 +135,8 @@ __global__ __launch_bounds__(kDkdvThreads, 1) void bwd_dkdv_kernel(BwdParams p) 
   __shared__ __bf16 q_lo[kUnit], q_hi[kUnit], do_lo[kUnit], do_hi[kUnit];
   // LSE (log2 domain) and Delta of a half, slot 32 blk + m = query
   // 32 blk + tok_perm(m) (accumulator-row order).
-  __shared__ float lse_lo[64], lse_hi[64], dl_lo[64], dl_hi[64];
+  // (16-byte aligned: rows are read four at a time)
+  __shared__ __align__(16) float lse_lo[64], lse_hi[64], dl_lo[64], dl_hi[64];
   __shared__ uint4 dma_scratch[64];
 
   const int hk = blockIdx.x, b = blockIdx.z;
@@ -244,16 +258,15 @@ __global__ __launch_bounds__(kDkdvThreads, 1) void bwd_dkdv_kernel(BwdParams p) 
     // the pair's sign-extended mask bit, after the exponential.  Only a
     // mixed block can hold a fully masked row (LSE = -inf), whose
     // exp2(+inf) is cleared the same way; every other row has a finite LSE.
+    const f32x16 lrow = acc_rows(lu + rb, g), drow = acc_rows(dlu + rb, g);
     if (mixed) {
-      const uint32_t wg = w >> g;
-      keep_masked(sacc, wg, lu + rb, dlu + rb, dpacc, c, g);
+      keep_masked(sacc, w >> g, lrow, drow, dpacc, c);
     } else {
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        const int qr = rb + acc_row(i, g);
-        const float pv = fast_exp2(fmaf(sacc[i], c, -lu[qr]));
+        const float pv = fast_exp2(fmaf(sacc[i], c, -lrow[i]));
         sacc[i] = pv;                                 // P
-        dpacc[i] = pv * (dpacc[i] - dlu[qr]);         // dS
+        dpacc[i] = pv * (dpacc[i] - drow[i]);         // dS
       }
     }
     // dV^T += dO^T P, dK^T += Q^T dS (contraction over the 32 queries).

@@ -3,12 +3,16 @@
     python -m tagseq2tagseq_amd.rocprof_summary trace  <kt_dir> <bench_json> <config> [bench args] > kernel_trace.txt
     python -m tagseq2tagseq_amd.rocprof_summary traffic <fetch_dir> <write_dir> \
         <copy_fetch_dir> <copy_write_dir> <config> > hbm_traffic.txt
-    python -m tagseq2tagseq_amd.rocprof_summary insts <sq_dir> <config> [bench args] > insts.txt
+    python -m tagseq2tagseq_amd.rocprof_summary insts <sq_dir> <kt_dir> <config> [bench args] > insts.txt
 
 `insts` reads one `--pmc` pass of SQ instruction counters (SQ_INSTS_VALU,
 SQ_INSTS_MFMA, SQ_INSTS_LDS, SQ_INSTS_SALU, SQ_INSTS_VALU_TRANS_F32,
 SQ_INSTS_VMEM, SQ_VALU_MFMA_BUSY_CYCLES, SQ_BUSY_CYCLES) and lists, per
-kernel, the instructions issued per MFMA.
+kernel, the instructions issued per MFMA and the MFMA-busy fraction:
+SQ_VALU_MFMA_BUSY_CYCLES per dispatch (summed over the chip) over the
+machine's SIMD-cycles in the kernel's mean duration from the kernel-trace
+run of the same session (1024 SIMDs at 2.4 GHz).  bench.py attaches the
+`mfma_busy` lines of this file to its JSON line.
 
 `trace` reads a `rocprofv3 --kernel-trace` database and lists, per kernel,
 the number of dispatches and their mean / median / min / max duration next to
@@ -166,9 +170,14 @@ INST_COUNTERS = ["SQ_INSTS_VALU", "SQ_INSTS_MFMA", "SQ_INSTS_LDS", "SQ_INSTS_SAL
                  "SQ_BUSY_CYCLES"]
 
 
-def insts(sq_dir: str, cfg: str, bench_args: str = "") -> str:
+SIMDS = 1024          # MI355X: 256 CUs x 4 SIMDs
+CLOCK_HZ = 2.4e9      # peak engine clock (the dense-peak figure uses the same)
+
+
+def insts(sq_dir: str, kt_dir: str, cfg: str, bench_args: str = "") -> str:
     bench_args = bench_args or f"--config {cfg} --no-cpu-baseline --steps 2 --warmup 1 --reps 2"
     means = {c: counter_means(sq_dir, c) for c in INST_COUNTERS}
+    durs = {k: statistics.mean(v) for k, v in kernel_durations(kt_dir).items()}
     lines = [
         f"# SQ instruction counters per dispatch -- {_label(cfg)} ({WORKLOADS.get(str(cfg), '?')}), MI355X",
         "#",
@@ -178,11 +187,13 @@ def insts(sq_dir: str, cfg: str, bench_args: str = "") -> str:
         "# instructions issued per MFMA: SQ_INSTS_VALU as counted (whether it includes the",
         "# MFMA instructions themselves is not separated here), transcendental VALU, LDS,",
         "# SALU and vector-memory instructions; MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES summed",
-        "# over the dispatch.",
+        "# over the dispatch; busy frac = that / (1024 SIMDs x 2.4 GHz x the kernel's mean",
+        f"# duration in the kernel-trace run {kt_dir} of the same session).",
         "",
         f"{'kernel':28s} {'MFMA':>10s} {'VALU/MFMA':>10s} {'TRANS/MFMA':>11s} {'LDS/MFMA':>9s} "
-        f"{'SALU/MFMA':>10s} {'VMEM/MFMA':>10s} {'MFMA busy':>12s}",
+        f"{'SALU/MFMA':>10s} {'VMEM/MFMA':>10s} {'MFMA busy':>12s} {'mean us':>9s} {'busy frac':>9s}",
     ]
+    fracs = {}
     kernels = sorted(means["SQ_INSTS_MFMA"], key=lambda k: -means["SQ_INSTS_MFMA"][k])
     for k in kernels:
         mf = means["SQ_INSTS_MFMA"].get(k, 0.0)
@@ -192,15 +203,42 @@ def insts(sq_dir: str, cfg: str, bench_args: str = "") -> str:
         lines.append(f"{k:28s} {mf:10.0f} {g('SQ_INSTS_VALU'):10.2f} "
                      f"{g('SQ_INSTS_VALU_TRANS_F32'):11.2f} {g('SQ_INSTS_LDS'):9.2f} "
                      f"{g('SQ_INSTS_SALU'):10.2f} {g('SQ_INSTS_VMEM'):10.2f} "
-                     f"{means['SQ_VALU_MFMA_BUSY_CYCLES'].get(k, 0.0):12.0f}")
+                     f"{means['SQ_VALU_MFMA_BUSY_CYCLES'].get(k, 0.0):12.0f} "
+                     f"{durs.get(k, float('nan')):9.1f} {_busy_frac(means, durs, k):9.4f}")
+        if k in durs:
+            fracs[k] = _busy_frac(means, durs, k)
+    lines.append("")
+    for k, f in fracs.items():
+        lines.append(f"mfma_busy {k}={f:.4f}")
     return "\n".join(lines) + "\n"
+
+
+def _busy_frac(means, durs, k) -> float:
+    d = durs.get(k)
+    if not d:
+        return float("nan")
+    return means["SQ_VALU_MFMA_BUSY_CYCLES"].get(k, 0.0) / (SIMDS * CLOCK_HZ * d * 1e-6)
+
+
+def read_mfma_busy(path: str) -> Dict[str, float]:
+    """The `mfma_busy <kernel>=<frac>` lines of an `insts` summary."""
+    out: Dict[str, float] = {}
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("mfma_busy "):
+                    k, v = line[len("mfma_busy "):].strip().split("=")
+                    out[k] = float(v)
+    except FileNotFoundError:
+        pass
+    return out
 
 
 def main(argv: List[str]) -> None:
     if len(argv) >= 4 and argv[0] == "trace":
         sys.stdout.write(trace(argv[1], argv[2], argv[3], " ".join(argv[4:])))
-    elif len(argv) >= 3 and argv[0] == "insts":
-        sys.stdout.write(insts(argv[1], argv[2], " ".join(argv[3:])))
+    elif len(argv) >= 4 and argv[0] == "insts":
+        sys.stdout.write(insts(argv[1], argv[2], argv[3], " ".join(argv[4:])))
     elif len(argv) >= 6 and argv[0] == "traffic":
         sys.stdout.write(traffic(argv[1], argv[2], argv[3], argv[4], argv[5], " ".join(argv[6:])))
     else:
