@@ -156,14 +156,6 @@ __global__ __launch_bounds__(kDkdvThreads, 1) void bwd_dkdv_kernel(BwdParams p) 
   const bool kvalid = key < T;
   const float c = p.scale_log2;
 
-  // K and V of the key tile stay in LDS; lane (g, n) reads row kloc as the B
-  // operand (k = d, n = key) of S = Q K^T and dP = dO V^T.  (The first
-  // barrier of the loop publishes them.)
-  load_tile_lds<D, kDkdvThreads>(k_s, slice_rsrc(p.k + b * p.k_sb + hk * p.k_sh, p.k_st, T, D),
-                                 p.k_st, k0, tid);
-  load_tile_lds<D, kDkdvThreads>(v_s, slice_rsrc(p.v + b * p.v_sb + hk * p.v_sh, p.v_st, T, D),
-                                 p.v_st, k0, tid);
-
   const size_t col = (size_t)mb * nt + kt;
   const int npart = uniform(p.m.q_num[col]);
   const int nfull = uniform(p.m.full_q_num[col]);
@@ -193,6 +185,29 @@ __global__ __launch_bounds__(kDkdvThreads, 1) void bwd_dkdv_kernel(BwdParams p) 
                      it < npart ? pslot[it] : 0);
   };
   int2 list_v = load_chunk(0);
+
+  // K and V of the key tile stay in LDS; lane (g, n) reads row kloc as the B
+  // operand (k = d, n = key) of S = Q K^T and dP = dO V^T.  They travel as
+  // direct global->LDS copies (two 64-row units each) issued after the query
+  // tile list and before the first Q / dO half, so the three are in flight
+  // together; the first barrier of the loop publishes them.
+  {
+    int koff[U::kPerWave + 1], voff[U::kPerWave + 1];
+#pragma unroll
+    for (int j = 0; j < U::kPerWave; ++j) {
+      koff[j] = unit_dma_offset<D>(wave + kDkdvWaves * j, p.k_st, lane);
+      voff[j] = unit_dma_offset<D>(wave + kDkdvWaves * j, p.v_st, lane);
+    }
+    koff[U::kPerWave] = unit_dma_offset<D>(U::kInsts - 1, p.k_st, lane);
+    voff[U::kPerWave] = unit_dma_offset<D>(U::kInsts - 1, p.v_st, lane);
+    const auto krs = slice_rsrc(p.k + b * p.k_sb + hk * p.k_sh, p.k_st, T, D);
+    const auto vrs = slice_rsrc(p.v + b * p.v_sb + hk * p.v_sh, p.v_st, T, D);
+    const int kr2 = (int)p.k_st * 2, vr2 = (int)p.v_st * 2;
+    unit_dma<D, kDkdvWaves>(k_s, krs, koff, k0 * kr2, wave, 4, dma_scratch);
+    unit_dma<D, kDkdvWaves>(k_s + kUnit, krs, koff, (k0 + 64) * kr2, wave, 5, dma_scratch);
+    unit_dma<D, kDkdvWaves>(v_s, vrs, voff, k0 * vr2, wave, 6, dma_scratch);
+    unit_dma<D, kDkdvWaves>(v_s + kUnit, vrs, voff, (k0 + 64) * vr2, wave, 7, dma_scratch);
+  }
   auto entry = [&](int it) {
     if ((it >> 6) != chunk) {
       chunk = it >> 6;

@@ -221,29 +221,4 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t slice_rsrc(const __bf16* base,
                                            0x00020000);
 }
 
-// Copy token rows [t0, t0 + 128) of a slice into a padded LDS tile; rows
-// past the slice end read as zeros.  Each thread moves 16-byte chunks; a wave
-// covers four whole rows.
-template <int D, int NTHREADS = kThreads>
-__device__ __forceinline__ void load_tile_lds(__bf16* dst, __amdgpu_buffer_rsrc_t src,
-                                              int64_t st, int t0, int tid) {
-  constexpr int kChunks = D / 8;
-  constexpr int kIters = kTile * kChunks / NTHREADS;
-  const int soff = (int)((int64_t)t0 * st * 2);
-  uint4 buf[kIters];
-#pragma unroll
-  for (int it = 0; it < kIters; ++it) {
-    const int c = tid + it * NTHREADS;
-    const int r = c / kChunks, col = (c % kChunks) * 8;
-    buf[it] = __builtin_bit_cast(
-        uint4, __builtin_amdgcn_raw_buffer_load_b128(src, (int)((r * st + col) * 2), soff, 0));
-  }
-#pragma unroll
-  for (int it = 0; it < kIters; ++it) {
-    const int c = tid + it * NTHREADS;
-    const int r = c / kChunks, col = (c % kChunks) * 8;
-    *reinterpret_cast<uint4*>(dst + r * pitch<D>() + col) = buf[it];
-  }
-}
-
 }  // namespace t2t
