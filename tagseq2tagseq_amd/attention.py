@@ -35,7 +35,7 @@ import torch.nn as nn
 from . import _lib
 from typing import List, Tuple
 
-from .block_mask import T2TBlockMask, tables_c_struct
+from .block_mask import T2TBlockMask, from_torch_block_mask, tables_c_struct
 
 LN2 = math.log(2.0)
 _DTYPE_CODES = {torch.bfloat16: _lib.T2T_DTYPE_BF16, torch.float32: _lib.T2T_DTYPE_F32}
@@ -55,11 +55,29 @@ def _view(t: torch.Tensor) -> _lib.T2TTensor:
     return s
 
 
+def as_t2t_block_mask(block_mask):
+    """A T2TBlockMask, or a torch BlockMask converted once
+    (block_mask.from_torch_block_mask) and kept on the BlockMask object, so
+    that every layer of a step reuses the conversion."""
+    if isinstance(block_mask, T2TBlockMask):
+        return block_mask
+    from torch.nn.attention.flex_attention import BlockMask
+    if not isinstance(block_mask, BlockMask):
+        raise TypeError(f"block_mask must be a T2TBlockMask or a torch BlockMask, "
+                        f"got {type(block_mask).__name__}")
+    conv = getattr(block_mask, "_t2t_block_mask", None)
+    if conv is None:
+        conv = from_torch_block_mask(block_mask)
+        block_mask._t2t_block_mask = conv
+    return conv
+
+
 def _validate(q, k, v, block_mask, enable_gqa):
     """Shape rules of torch/nn/attention/flex_attention.py:1473-1541."""
     if not isinstance(block_mask, T2TBlockMask):
         raise TypeError("block_mask must be a T2TBlockMask (build one with the mask creators "
-                        "in tagseq2tagseq_amd.mask_creators)")
+                        "in tagseq2tagseq_amd.mask_creators, or pass a torch BlockMask to "
+                        "flex_attention)")
     if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
         raise ValueError("query, key, value must be 4-D [B, H, T, D]")
     if not (q.dtype == k.dtype == v.dtype):
@@ -270,6 +288,11 @@ def flex_attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
     """Drop-in for torch's flex_attention on the doc_causal / cross_doc_link
     path (torch/nn/attention/flex_attention.py:1396-1676).
 
+    ``block_mask`` is a T2TBlockMask from this package's mask creators or a
+    torch BlockMask (128 x 128 tiles, one mask for every head, e.g. from
+    create_block_mask); the latter is converted once and the conversion kept
+    on it (as_t2t_block_mask).
+
     ``score_mod`` must be None (the reference passes none).  The returned LSE is
     in natural log, as torch's (internal log2 value times ln 2, :1575-1600).
     """
@@ -277,6 +300,9 @@ def flex_attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
         raise NotImplementedError("score_mod is not supported by the gfx950 masked-attention path")
     if block_mask is None:
         raise ValueError("block_mask is required (build it with tagseq2tagseq_amd.mask_creators)")
+    if not query.is_cuda:
+        raise RuntimeError("the masked-attention kernels need ROCm GPU tensors")
+    block_mask = as_t2t_block_mask(block_mask)
     _, _, _, _, D = _validate(query, key, value, block_mask, enable_gqa)
     if scale is None:
         scale = 1.0 / math.sqrt(D)  # torch/nn/attention/flex_attention.py:1544

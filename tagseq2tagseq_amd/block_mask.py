@@ -14,13 +14,16 @@ for element masking.
 
 ``to_block_mask()`` rebuilds a torch ``BlockMask`` from the same tables (via
 ``BlockMask.from_kv_blocks``) for interoperability with torch's own
-flex_attention.
+flex_attention, and ``from_torch_block_mask()`` goes the other way: a torch
+``BlockMask`` (128 x 128 tiles, one mask for every head) becomes a
+``T2TBlockMask`` over its own KV tables, with the partial tiles' bitmaps
+evaluated from its ``mask_mod``.
 """
 from __future__ import annotations
 
 import ctypes
 from dataclasses import dataclass, field
-from typing import Optional
+from typing import Callable, Optional
 
 import torch
 
@@ -51,6 +54,9 @@ class T2TBlockMask:
     tile_bits: torch.Tensor        # int32 [slots, 2, 128, 4]
     BLOCK_SIZE: tuple = (TILE, TILE)
     _c: Optional[_lib.T2TBlockMaskC] = field(default=None, repr=False)
+    # mask_mod of the torch BlockMask this mask was converted from (its
+    # per-token inputs are then unknown: doc_ids are zeros and words 0)
+    source_mask_mod: Optional[Callable] = field(default=None, repr=False)
 
     @property
     def mask_batch(self) -> int:
@@ -86,7 +92,10 @@ class T2TBlockMask:
 
     def mask_mod(self):
         """The reference's mask_mod over this mask's per-token tensors
-        (cross_doc_mask.py:348-357; doc_causal when there are no words)."""
+        (cross_doc_mask.py:348-357; doc_causal when there are no words), or
+        the source BlockMask's own mask_mod for a converted mask."""
+        if self.source_mask_mod is not None:
+            return self.source_mask_mod
         doc, qb, kb = self.doc_ids, self.q_bits, self.kv_bits
         W = self.words
 
@@ -218,3 +227,112 @@ def build_block_mask(doc_ids: torch.Tensor, q_bits: Optional[torch.Tensor] = Non
         full_q_num_blocks=t["full_q_num"], full_q_indices=t["full_q_idx"],
         row_order=row_order, col_order=col_order, kv_bits_off=kv_bits_off,
         q_bits_slot=q_bits_slot, tile_bits=tile_bits, _c=cs)
+
+
+def _ordered(flags: torch.Tensor):
+    """(count, order) of a [..., n] bool tensor: the number of set entries and
+    their indices ascending followed by the unset ones ascending (torch's
+    _dense_to_ordered convention, torch/nn/attention/flex_attention.py:429-436)."""
+    n = flags.shape[-1]
+    key = (~flags).to(torch.int64) * n + torch.arange(n, device=flags.device)
+    return flags.sum(-1, dtype=torch.int32), key.argsort(-1).to(torch.int32)
+
+
+def _rank_desc(count: torch.Tensor) -> torch.Tensor:
+    """Indices by descending count, ties by higher index first (the launch
+    orders of the metadata pass)."""
+    n = count.shape[-1]
+    key = count.to(torch.int64) * n + torch.arange(n, device=count.device)
+    return key.argsort(-1, descending=True).to(torch.int32)
+
+
+def _pack_bits(m: torch.Tensor) -> torch.Tensor:
+    """[P, 128, 128] bool -> int32 [P, 128, 4]: bit j of word w of row r is
+    m[r, 32 w + j]."""
+    P = m.shape[0]
+    w = m.reshape(P, TILE, 4, 32).to(torch.int64) << torch.arange(32, device=m.device)
+    return w.sum(-1).to(torch.int32)
+
+
+def from_torch_block_mask(bm, tile_chunk: int = 256) -> T2TBlockMask:
+    """A T2TBlockMask over a torch BlockMask's own tables (kv_num_blocks,
+    kv_indices, full_kv_num_blocks, full_kv_indices define the tile classes;
+    torch/nn/attention/flex_attention.py:586-657), for the flex_attention seam
+    when the caller brings a mask made by torch's create_block_mask.  The
+    column tables, launch orders and bitmap slots are derived with torch ops
+    on the mask's device, and the allowed-pair bitmap of every partial tile is
+    evaluated from ``bm.mask_mod`` at head 0 over the tile's valid positions
+    (positions past the sequence are masked, as create_block_mask pads).
+    Requires 128 x 128 tiles, equal query and key lengths and one mask for
+    every head (a head dimension of 1)."""
+    if tuple(bm.BLOCK_SIZE) != (TILE, TILE):
+        raise ValueError(f"BlockMask tiles {tuple(bm.BLOCK_SIZE)} are not {TILE} x {TILE}")
+    Tq, Tk = bm.seq_lengths
+    if Tq != Tk:
+        raise ValueError(f"self-attention masks only (Q_LEN {Tq} != KV_LEN {Tk})")
+    kvn = bm.kv_num_blocks
+    if kvn.dim() != 3 or kvn.shape[1] != 1:
+        raise ValueError("per-head block masks are not supported (the head dimension must be 1)")
+    T, dev = int(Tq), kvn.device
+    Bm, nt = int(kvn.shape[0]), int(kvn.shape[-1])
+    if nt != (T + TILE - 1) // TILE:
+        raise ValueError(f"BlockMask has {nt} tile columns for length {T}")
+    i32 = dict(dtype=torch.int32, device=dev)
+    ar = torch.arange(nt, device=dev)
+    cls = torch.zeros((Bm, nt, nt), dtype=torch.int8, device=dev)
+
+    def mark(num, idx, value):
+        if num is None:
+            return
+        num, idx = num[:, 0].to(torch.int64), idx[:, 0, :, :nt].to(torch.int64)
+        live = ar[None, None, :] < num[:, :, None]
+        rows = ar[None, :, None].expand(Bm, nt, nt)
+        bsel = torch.arange(Bm, device=dev)[:, None, None].expand(Bm, nt, nt)
+        cls[bsel[live], rows[live], idx[live]] = value
+
+    mark(bm.kv_num_blocks, bm.kv_indices, 1)
+    mark(bm.full_kv_num_blocks, bm.full_kv_indices, 2)
+    part, full = cls == 1, cls == 2
+    kv_num, kv_idx = _ordered(part)
+    fkv_num, fkv_idx = _ordered(full)
+    q_num, q_idx = _ordered(part.transpose(1, 2))
+    fq_num, fq_idx = _ordered(full.transpose(1, 2))
+    row_order = _rank_desc(kv_num + fkv_num)
+    col_order = _rank_desc(q_num + fq_num)
+    flat = kv_num.reshape(-1).to(torch.int64)
+    kv_bits_off = (torch.cumsum(flat, 0) - flat).reshape(Bm, nt).to(torch.int32)
+    # slot of partial tile (b, r, c): the row's first slot + its rank in the row
+    rank = torch.cumsum(part.to(torch.int32), -1) - 1
+    slot_grid = torch.where(part, kv_bits_off[:, :, None] + rank, torch.zeros_like(rank))
+    q_bits_slot = torch.gather(slot_grid.transpose(1, 2), 2, q_idx.to(torch.int64))
+    q_bits_slot = torch.where(ar[None, None, :] < q_num[:, :, None], q_bits_slot,
+                              torch.zeros_like(q_bits_slot)).to(torch.int32)
+    # bitmaps of the partial tiles, in slot order (row-major enumeration)
+    pb, pr, pc = part.nonzero(as_tuple=True)
+    P = int(pb.numel())
+    tile_bits = torch.zeros((max(1, P), 2, TILE, 4), **i32)
+    t = torch.arange(TILE, device=dev)
+    for s0 in range(0, P, tile_chunk):
+        b_, r_, c_ = (x[s0:s0 + tile_chunk] for x in (pb, pr, pc))
+        qpos = r_[:, None, None] * TILE + t[None, :, None]
+        kpos = c_[:, None, None] * TILE + t[None, None, :]
+        ok = (qpos < T) & (kpos < T)
+        m = bm.mask_mod(b_[:, None, None], torch.zeros_like(b_)[:, None, None],
+                        qpos.clamp(max=T - 1), kpos.clamp(max=T - 1))
+        m = torch.as_tensor(m, device=dev).expand(ok.shape) & ok
+        tile_bits[s0:s0 + tile_chunk, 0] = _pack_bits(m)
+        tile_bits[s0:s0 + tile_chunk, 1] = _pack_bits(m.transpose(1, 2))
+    out = T2TBlockMask(
+        seq_len=T, doc_ids=torch.zeros((Bm, T), **i32),
+        q_bits=torch.zeros((Bm, 0, T), dtype=torch.int64, device=dev),
+        kv_bits=torch.zeros((Bm, 0, T), dtype=torch.int64, device=dev), tile_class=cls,
+        kv_num_blocks=kv_num[:, None].contiguous(), kv_indices=kv_idx[:, None].contiguous(),
+        full_kv_num_blocks=fkv_num[:, None].contiguous(),
+        full_kv_indices=fkv_idx[:, None].contiguous(),
+        q_num_blocks=q_num[:, None].contiguous(), q_indices=q_idx[:, None].contiguous(),
+        full_q_num_blocks=fq_num[:, None].contiguous(),
+        full_q_indices=fq_idx[:, None].contiguous(),
+        row_order=row_order.contiguous(), col_order=col_order.contiguous(),
+        kv_bits_off=kv_bits_off.contiguous(), q_bits_slot=q_bits_slot.contiguous(),
+        tile_bits=tile_bits, source_mask_mod=bm.mask_mod)
+    return out

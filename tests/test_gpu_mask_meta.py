@@ -8,75 +8,11 @@ from oracle import mask_oracle as mo
 from oracle import tile_oracle
 from tagseq2tagseq_amd import synth
 from tagseq2tagseq_amd.block_mask import build_block_mask
+from tests.helpers import TABLES
+from tests.helpers import check_block_mask as _check
 from tests.helpers import random_row, row_arrays, to_dev_words
 
 pytestmark = pytest.mark.gpu
-
-TABLES = ["kv_num_blocks", "kv_indices", "full_kv_num_blocks", "full_kv_indices",
-          "q_num_blocks", "q_indices", "full_q_num_blocks", "full_q_indices"]
-
-
-def _pack_bits(tile: np.ndarray) -> np.ndarray:
-    """bool [128, 128] -> uint32 [128, 4], bit j of word w = tile[r, 32 w + j]."""
-    return np.packbits(tile, axis=1, bitorder="little").view("<u4").reshape(128, 4)
-
-
-def _check_extras(bm, b, doc, qb, kb, label):
-    """Launch orders, bitmap slots and partial-tile bitmaps against the oracle."""
-    T = doc.shape[0]
-    nt = (T + 127) // 128
-    kv_num = bm.kv_num_blocks[b, 0].cpu().numpy()
-    full_num = bm.full_kv_num_blocks[b, 0].cpu().numpy()
-    kv_idx = bm.kv_indices[b, 0].cpu().numpy()
-    q_num = bm.q_num_blocks[b, 0].cpu().numpy()
-    q_full = bm.full_q_num_blocks[b, 0].cpu().numpy()
-    q_idx = bm.q_indices[b, 0].cpu().numpy()
-    row_order = bm.row_order[b].cpu().numpy()
-    col_order = bm.col_order[b].cpu().numpy()
-    off = bm.kv_bits_off[b].cpu().numpy()
-    slot_col = bm.q_bits_slot[b].cpu().numpy()
-    bits = bm.tile_bits.cpu().numpy()
-    assert sorted(row_order.tolist()) == list(range(nt)), f"{label}: row_order not a permutation"
-    assert sorted(col_order.tolist()) == list(range(nt)), f"{label}: col_order not a permutation"
-    rc = (kv_num + full_num)[row_order]
-    cc = (q_num + q_full)[col_order]
-    assert (np.diff(rc) <= 0).all() and (np.diff(cc) <= 0).all(), f"{label}: orders not longest-first"
-    base = int(bm.kv_num_blocks[:b].sum().item())
-    exp_off = base + np.concatenate([[0], np.cumsum(kv_num)[:-1]])
-    np.testing.assert_array_equal(off, exp_off, err_msg=f"{label}: kv_bits_off")
-    row_slot = {}
-    pad = nt * 128 - T
-    for qt in range(nt):
-        if kv_num[qt] == 0:
-            continue
-        rows = mo.dense_mask(doc, qb, kb, (qt * 128, min(T, qt * 128 + 128)))
-        rows = np.pad(rows, ((0, 128 - rows.shape[0]), (0, pad)))
-        for i in range(kv_num[qt]):
-            kt = kv_idx[qt, i]
-            slot = off[qt] + i
-            row_slot[(qt, kt)] = slot
-            tile = rows[:, kt * 128:(kt + 1) * 128]
-            np.testing.assert_array_equal(bits[slot, 0].view("<u4"), _pack_bits(tile),
-                                          err_msg=f"{label}: row bits tile ({qt},{kt})")
-            np.testing.assert_array_equal(bits[slot, 1].view("<u4"), _pack_bits(tile.T.copy()),
-                                          err_msg=f"{label}: column bits tile ({qt},{kt})")
-    for kt in range(nt):
-        for i in range(q_num[kt]):
-            assert slot_col[kt, i] == row_slot[(q_idx[kt, i], kt)], f"{label}: q_bits_slot ({kt},{i})"
-
-
-def _check(bm, rows_np, label):
-    tc = bm.tile_class.cpu().numpy()
-    got = {name: getattr(bm, name).cpu().numpy() for name in TABLES}
-    for b, (doc, qb, kb) in enumerate(rows_np):
-        counts = tile_oracle.tile_counts(doc, qb, kb)
-        ref = mo.block_mask_tables(doc, qb, kb, counts=counts)
-        exp_cls = ref["partial"] + 2 * ref["full"]
-        np.testing.assert_array_equal(tc[b], exp_cls, err_msg=f"{label} b={b}: tile classes")
-        for name in TABLES:
-            np.testing.assert_array_equal(got[name][b, 0], ref[name], err_msg=f"{label} b={b}: {name}")
-        _check_extras(bm, b, doc, qb, kb, f"{label} b={b}")
-
 
 def _run(rows_np, device, label):
     doc = torch.stack([torch.from_numpy(r[0]) for r in rows_np]).to(device)
