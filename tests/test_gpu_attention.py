@@ -142,10 +142,12 @@ def test_full_size_against_torch_fp32(cfg, gpu_device):
     bm = _mask_from_rows(rows, gpu_device)
     q, k, v, do = _inputs(B, Hq, Hkv, T, D, cfg, gpu_device)
     q.requires_grad_(True); k.requires_grad_(True); v.requires_grad_(True)
-    out = flex_attention(q, k, v, block_mask=bm, enable_gqa=Hq != Hkv)
+    out, lse = flex_attention(q, k, v, block_mask=bm, enable_gqa=Hq != Hkv, return_lse=True)
     out.backward(do)
     G = Hq // Hkv
-    heads = list(range(G)) if G > 1 else [0, Hq - 1]  # a whole GQA group -> exact dk/dv
+    # config 3 (the metric's workload): every head; otherwise a whole GQA
+    # group (exact dk / dv) or the first and last head
+    heads = list(range(Hq)) if cfg == 3 else list(range(G)) if G > 1 else [0, Hq - 1]
     masks = []
     for r in rows:
         masks.append((torch.from_numpy(r[0]).to(gpu_device), to_dev_words(r[1], gpu_device),
@@ -153,6 +155,7 @@ def test_full_size_against_torch_fp32(cfg, gpu_device):
     ref = torch_ref_attention(q.detach(), k.detach(), v.detach(), do, masks, heads=heads)
     for (b, h), o_ref in ref["o"].items():
         assert_close(out[b, h].detach(), o_ref, ATOL, RTOL, f"cfg{cfg} out b{b} h{h}")
+        assert_close(lse[b, h].detach(), ref["lse"][(b, h)], 1e-3, 1e-3, f"cfg{cfg} lse b{b} h{h}")
         assert_close(q.grad[b, h], ref["dq"][(b, h)], ATOL, RTOL, f"cfg{cfg} dq b{b} h{h}")
     # each checked KV head has all of its query heads evaluated -> complete dk / dv
     for (b, hk), dk_ref in ref["dk"].items():
