@@ -113,7 +113,7 @@ def trace(kt_dir: str, bench_json: str, cfg: str, bench_args: str = "") -> str:
         "#",
         "# command (repo root, GPU box):",
         f"#   rocprofv3 --kernel-trace --stats -d {kt_dir} -o {out_name} -- \\",
-        f"#       python -u bench.py {bench_args}",
+        f"#       python3 -u bench.py {bench_args}",
         "# durations in microseconds over every dispatch of the run (warm-up, timed steps and",
         "# bench.py's per-kernel timing loops); the last column is bench.py's own HIP-event",
         "# mean per call from the JSON line of the same profiled run (token_inputs: the whole",
@@ -147,11 +147,11 @@ def traffic(fetch_dir: str, write_dir: str, cfetch_dir: str, cwrite_dir: str, cf
         f"# HBM traffic per launch -- {_label(cfg)} ({WORKLOADS.get(str(cfg), '?')}), MI355X",
         "#",
         "# commands (repo root, GPU box), one counter per pass:",
-        f"#   rocprofv3 --pmc FETCH_SIZE -d {fetch_dir} -o f -- python -u bench.py {bench_args}",
-        f"#   rocprofv3 --pmc WRITE_SIZE -d {write_dir} -o w -- python -u bench.py {bench_args}",
+        f"#   rocprofv3 --pmc FETCH_SIZE -d {fetch_dir} -o f -- python3 -u bench.py {bench_args}",
+        f"#   rocprofv3 --pmc WRITE_SIZE -d {write_dir} -o w -- python3 -u bench.py {bench_args}",
         "# calibration: the same counters on bench.py --copy-calibration (1 GiB device copies):",
-        f"#   rocprofv3 --pmc FETCH_SIZE -d {cfetch_dir} -o cf -- python -u bench.py --copy-calibration",
-        f"#   rocprofv3 --pmc WRITE_SIZE -d {cwrite_dir} -o cw -- python -u bench.py --copy-calibration",
+        f"#   rocprofv3 --pmc FETCH_SIZE -d {cfetch_dir} -o cf -- python3 -u bench.py --copy-calibration",
+        f"#   rocprofv3 --pmc WRITE_SIZE -d {cwrite_dir} -o cw -- python3 -u bench.py --copy-calibration",
         f"# copy of {copy_kib:.0f} KiB: factors fetch {ff:.4f}, write {wf:.4f}",
         "# traffic_bytes = (FETCH_SIZE * fetch_factor + WRITE_SIZE * write_factor) * 1024, mean per dispatch",
         "",
@@ -183,7 +183,7 @@ def insts(sq_dir: str, kt_dir: str, cfg: str, bench_args: str = "") -> str:
         "#",
         "# command (repo root, GPU box), one pass:",
         f"#   rocprofv3 --pmc {' '.join(INST_COUNTERS)} -d {sq_dir} -o sq -- \\",
-        f"#       python -u bench.py {bench_args}",
+        f"#       python3 -u bench.py {bench_args}",
         "# instructions issued per MFMA: SQ_INSTS_VALU as counted (whether it includes the",
         "# MFMA instructions themselves is not separated here), transcendental VALU, LDS,",
         "# SALU and vector-memory instructions; MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES summed",
