@@ -394,13 +394,15 @@ __global__ __launch_bounds__(kThreads, 2) void bwd_dq_kernel(BwdParams p) {
   __shared__ uint32_t bits_lds[2][kTile * 4];
   __shared__ uint4 dma_scratch[64];  // sink of the copies no wave owns
 
-  const int h = blockIdx.x, b = blockIdx.z;
+  const int b = blockIdx.z;
   const int tid = threadIdx.x, wave = uniform(tid >> 6), lane = tid & 63;
   const int g = lane >> 5, n = lane & 31;
+  const int T = p.T, nt = p.m.nt;
+  int h, slot;
+  head_and_slot(p.Hq, p.Hkv, nt, h, slot);
   const int hk = h / (p.Hq / p.Hkv);
   const int mb = p.m.Bm > 1 ? b : 0;
-  const int T = p.T, nt = p.m.nt;
-  const int qt = uniform(p.m.row_order[(size_t)mb * nt + blockIdx.y]);
+  const int qt = uniform(p.m.row_order[(size_t)mb * nt + slot]);
   const int q0 = qt * kTile;
   const int qloc = 32 * wave + n;
   const int qrow = q0 + qloc;

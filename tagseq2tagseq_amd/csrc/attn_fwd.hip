@@ -26,9 +26,9 @@
 // barrier that retired them, together with the next tile's bitmap; one
 // barrier per half.  No staging registers and no register->LDS stores.
 //
-// Work-groups are dispatched longest row first (row_order) with the head as
-// the fastest grid dimension, so the heads sharing an XCD (blockIdx.x mod 8)
-// stream the same K/V through that XCD's L2.
+// Work-groups are dispatched longest row first (row_order); with grouped-query
+// heads the heads of one KV head and row run back to back on one XCD
+// (head_and_slot), so their K/V copies are served by that XCD's L2.
 #include "attn_kernels.h"
 
 namespace t2t {
@@ -58,13 +58,15 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(FwdParams p)
   __shared__ uint32_t bits_lds[2][kTile * 4];
   __shared__ uint4 dma_scratch[64];  // sink of the copies no wave owns
 
-  const int h = blockIdx.x, b = blockIdx.z;
+  const int b = blockIdx.z;
   const int tid = threadIdx.x, wave = uniform(tid >> 6), lane = tid & 63;
   const int g = lane >> 5, n = lane & 31;
+  const int T = p.T, nt = p.m.nt;
+  int h, slot;
+  head_and_slot(p.Hq, p.Hkv, nt, h, slot);
   const int hk = h / (p.Hq / p.Hkv);
   const int mb = p.m.Bm > 1 ? b : 0;
-  const int T = p.T, nt = p.m.nt;
-  const int qt = uniform(p.m.row_order[(size_t)mb * nt + blockIdx.y]);
+  const int qt = uniform(p.m.row_order[(size_t)mb * nt + slot]);
   const int q0 = qt * kTile;
   const int qloc = 32 * wave + n;  // query row within the tile
   const int qrow = q0 + qloc;

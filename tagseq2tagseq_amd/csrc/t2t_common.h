@@ -165,6 +165,28 @@ __device__ __forceinline__ constexpr int acc_row(int i, int g) {
 // Value known to be equal in every lane (lets the compiler keep it in SGPRs).
 __device__ __forceinline__ int uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
 
+// (query head h, launch-order position y) of this work-group in a grid of
+// (Hq, nt) blocks per batch row.  The hardware hands work-groups to the 8
+// XCDs round-robin in dispatch order.  With grouped-query heads (G = Hq / Hkv
+// > 1) the G heads that share a KV head and a query tile are placed 8
+// dispatch slots apart, so one XCD runs them back to back and its L2 serves
+// their identical K/V copies after the first; the groups themselves keep
+// launch order (KV head fastest).  Without grouping, or when the Hkv * nt
+// groups do not fill whole rounds of 8, heads stay the fastest dimension.
+__device__ __forceinline__ void head_and_slot(int Hq, int Hkv, int nt, int& h, int& y) {
+  const int G = Hq / Hkv;
+  if (G == 1 || ((Hkv * nt) & 7) != 0) {
+    h = blockIdx.x;
+    y = blockIdx.y;
+    return;
+  }
+  const int L = blockIdx.x + Hq * blockIdx.y;
+  const int round = L / (8 * G), r = L - round * 8 * G;
+  const int grp = 8 * round + (r & 7);  // (KV head, position) group
+  h = (grp % Hkv) * G + (r >> 3);
+  y = grp / Hkv;
+}
+
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // Combine x of lanes l and l ^ 32 (the two halves of a 32x32 accumulator
