@@ -174,33 +174,51 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(FwdParams p)
     __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
 
     __builtin_amdgcn_s_setprio(0);
-    float mx = -INFINITY;
+    // Probabilities against the current reference max come first.  The
+    // reference moves only when the row max exceeds it by 8 (log2 units),
+    // i.e. when a probability would exceed 2^8; a lane whose probabilities
+    // sum to at most 2^7 has none near that, so when every lane's sum is
+    // that small and every row has a finite reference, no row moves and the
+    // probabilities stand -- the row max is not needed at all.  Otherwise
+    // the row max decides as before, and rows that move rescale O and the
+    // sum and recompute their probabilities.  Either way the values are
+    // those of the max-first order.
+    auto probs = [&](bf16x8* pf) {
+      const float neg = m_ref == -INFINITY ? 0.f : -m_ref * c;
+      float rs = 0.f;
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+      for (int s = 0; s < 4; ++s)  // k-step s: entries [8 (s & 1), + 8) of block s >> 1
 #pragma unroll
-      for (int i = 0; i < 16; ++i) mx = fmaxf(mx, st[j][i]);
-    mx = halves_max(mx);
-    // The reference moves only when the row max exceeds it by 8 (log2
-    // units); -inf - -inf compares false, so untouched rows never move.
-    const bool move = (mx - m_ref) * c > 8.f;
-    if (__ballot(move) != 0ull) {
-      const float alpha = move ? fast_exp2((m_ref - mx) * c) : 1.f;  // 0 from -inf
-      l_run *= alpha;
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt) oacc[dt] *= alpha;
-      m_ref = move ? mx : m_ref;
-    }
-    const float neg = m_ref == -INFINITY ? 0.f : -m_ref * c;
-    float rs = 0.f;
+        for (int k = 0; k < 8; ++k) {
+          const float e = fast_exp2(fmaf(st[s >> 1][8 * (s & 1) + k], c, neg));
+          pf[s][k] = (__bf16)e;
+          rs += e;
+        }
+      return rs;
+    };
     bf16x8 pf[4];
+    float rs = probs(pf);
+    // (pins the first evaluation ahead of the branch; the compiler would
+    // otherwise move it into the branch's fall-through, behind the row max)
+    asm volatile("" ::"v"(pf[0]), "v"(pf[1]), "v"(pf[2]), "v"(pf[3]), "v"(rs));
+    if (__ballot(m_ref == -INFINITY || !(rs <= 128.f)) != 0ull) {
+      float mx = -INFINITY;
 #pragma unroll
-    for (int s = 0; s < 4; ++s)  // k-step s: entries [8 (s & 1), + 8) of block s >> 1
+      for (int j = 0; j < 2; ++j)
 #pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        const float e = fast_exp2(fmaf(st[s >> 1][8 * (s & 1) + k], c, neg));
-        pf[s][k] = (__bf16)e;
-        rs += e;
+        for (int i = 0; i < 16; ++i) mx = fmaxf(mx, st[j][i]);
+      mx = halves_max(mx);
+      // -inf - -inf compares false, so untouched rows never move.
+      const bool move = (mx - m_ref) * c > 8.f;
+      if (__ballot(move) != 0ull) {
+        const float alpha = move ? fast_exp2((m_ref - mx) * c) : 1.f;  // 0 from -inf
+        l_run *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) oacc[dt] *= alpha;
+        m_ref = move ? mx : m_ref;
+        rs = probs(pf);
       }
+    }
     l_run += halves_sum(rs);
 
     // O^T += V^T P^T, 16 keys per k-step.
