@@ -488,6 +488,8 @@ __global__ __launch_bounds__(kThreads, 2) void bwd_dq_kernel(BwdParams p) {
   f32x16 dqacc[DT];
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) dqacc[dt] = f32x16{};
+  // -Delta in every entry: the dP^T chains start from it and end at dP - Delta.
+  f32x16 dseed;
 
   // One 32-key block: rows 32 j .. 32 j + 31 of a half's units; w = the
   // lane's bitmap word (all ones for full tiles).
@@ -495,7 +497,7 @@ __global__ __launch_bounds__(kThreads, 2) void bwd_dq_kernel(BwdParams p) {
     if (__ballot(w != 0u) == 0ull) return;
     const bool mixed = __ballot(w != ~0u) != 0ull;
     f32x16 sacc = mixed ? mask_bias(~(w >> g)) : f32x16{};
-    f32x16 dpacc = f32x16{};
+    f32x16 dpacc = dseed;
     __builtin_amdgcn_s_setprio(1);  // MFMA runs at raised wave priority
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
@@ -516,7 +518,7 @@ __global__ __launch_bounds__(kThreads, 2) void bwd_dq_kernel(BwdParams p) {
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       const float pv = fast_exp2(fmaf(sacc[i], c, neg_lse));
-      dpacc[i] = pv * (dpacc[i] - delta);  // dS^T
+      dpacc[i] = pv * dpacc[i];  // dS^T
     }
     // dQ^T += K^T dS^T (contraction over the 32 keys of the block).
     __builtin_amdgcn_s_setprio(1);
@@ -548,6 +550,8 @@ __global__ __launch_bounds__(kThreads, 2) void bwd_dq_kernel(BwdParams p) {
     delta = halves_sum(acc);
     if (qvalid && g == 0) p.delta[rowstat] = delta;
   }
+#pragma unroll
+  for (int i = 0; i < 16; ++i) dseed[i] = -delta;
   for (int it = 0; it < ntiles; ++it) {
     const bool partial = it < npart;
     const int k0 = k0_next;
