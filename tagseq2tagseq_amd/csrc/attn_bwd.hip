@@ -79,19 +79,18 @@ __global__ __launch_bounds__(kThreads) void bwd_delta_kernel(BwdParams p) {
   if (rowid < nrows && sub == 0) p.delta[rowid] = acc;
 }
 
-// P and dS of a mixed dK/dV block in place (sacc -> P, dpacc = dP - Delta ->
-// dS) for a lane whose bitmap word, shifted right by its lane group, is wg:
-// P of a masked pair is cleared with the pair's sign-extended mask bit.  l:
-// the lane's 16 rows' LSE in accumulator order.
+// P and dS of a mixed dK/dV block in place (sacc = S - LSE / c -> P,
+// dpacc = dP - Delta -> dS) for a lane whose bitmap word, shifted right by
+// its lane group, is wg: P of a masked pair is cleared with the pair's
+// sign-extended mask bit.
 template <int I = 0>
-__device__ __forceinline__ void keep_masked(f32x16& sacc, uint32_t wg, const f32x16& l,
-                                            f32x16& dpacc, float c) {
+__device__ __forceinline__ void keep_masked(f32x16& sacc, uint32_t wg, f32x16& dpacc, float c) {
   if constexpr (I < 16) {
-    const float e = fast_exp2(fmaf(sacc[I], c, -l[I]));
+    const float e = fast_exp2(sacc[I] * c);
     const float pv = __int_as_float(__float_as_int(e) & sbfe1_c<acc_tok_bit(I)>(wg));
     sacc[I] = pv;
     dpacc[I] = pv * dpacc[I];
-    keep_masked<I + 1>(sacc, wg, l, dpacc, c);
+    keep_masked<I + 1>(sacc, wg, dpacc, c);
   }
 }
 
@@ -219,36 +218,39 @@ __global__ __launch_bounds__(kDkdvThreads, 1) void bwd_dkdv_kernel(BwdParams p) 
 
   // Copies of query rows [r0, r0 + 64) of head h into one half's units
   // (Q + LSE, dO + Delta).  LSE and Delta go one dword per lane, gathered
-  // into accumulator-row order; rows at or past T read zero.  Delta is
-  // staged negated, as the dP chains' starting value: wave 3 loads it into a
-  // register and stores -Delta into the half's slots just before the barrier
-  // that publishes the half (publish_delta), by which time the load has long
-  // landed.
+  // into accumulator-row order; rows at or past T read zero.  Both are
+  // staged as the starting values of the score and dP chains, -LSE / c and
+  // -Delta: waves 2 and 3 load them into a register and store the seeds
+  // into the half's slots just before the barrier that publishes the half
+  // (publish_rows), by which time the loads have long landed.
+  uint32_t row_pend = 0u;     // wave 2: LSE, wave 3: Delta bits of the half in flight
+  float* row_dst = nullptr;   // and its slot array (null: nothing pending)
+  const float inv_c = 1.f / c;
   auto load_q_part = [&](__bf16* qd, float* ld, int h, int r0) {
     const auto qrs = slice_rsrc(p.q + b * p.q_sb + h * p.q_sh, p.q_st, T, D);
     unit_dma<D, kDkdvWaves>(qd, qrs, qoff, r0 * (int)p.q_st * 2, wave, 0, dma_scratch);
     const auto lrs = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<float*>(p.lse2 + ((size_t)b * p.Hq + h) * T), 0, T * 4, 0x00020000);
-    if (wave == 2)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(lrs, (__attribute__((address_space(3))) void*)ld, 4,
-                                               (r0 + lrow) * 4, 0, 0, 0);
+    if (wave == 2) {
+      row_pend = __builtin_amdgcn_raw_buffer_load_b32(lrs, (r0 + lrow) * 4, 0, 0);
+      row_dst = ld;
+    }
   };
-  uint32_t dl_pend = 0u;     // wave 3: Delta bits of the half in flight
-  float* dl_dst = nullptr;   // and its slot array (null: nothing pending)
   auto load_do_part = [&](__bf16* dd, float* dld, int h, int r0) {
     const auto drs = slice_rsrc(p.dout + b * p.do_sb + h * p.do_sh, p.do_st, T, D);
     unit_dma<D, kDkdvWaves>(dd, drs, ooff, r0 * (int)p.do_st * 2, wave, 1, dma_scratch);
     const auto drs2 = __builtin_amdgcn_make_buffer_rsrc(p.delta + ((size_t)b * p.Hq + h) * T, 0,
                                                         T * 4, 0x00020000);
     if (wave == 3) {
-      dl_pend = __builtin_amdgcn_raw_buffer_load_b32(drs2, (r0 + lrow) * 4, 0, 0);
-      dl_dst = dld;
+      row_pend = __builtin_amdgcn_raw_buffer_load_b32(drs2, (r0 + lrow) * 4, 0, 0);
+      row_dst = dld;
     }
   };
-  auto publish_delta = [&]() {
-    if (wave == 3 && dl_dst != nullptr) {
-      dl_dst[lane] = -__uint_as_float(dl_pend);
-      dl_dst = nullptr;
+  auto publish_rows = [&]() {
+    if (row_dst != nullptr) {  // waves 2 and 3 only
+      const float x = __uint_as_float(row_pend);
+      row_dst[lane] = wave == 2 ? -x * inv_c : -x;
+      row_dst = nullptr;
     }
   };
   // The lane's bitmap words (its key, queries 32 w .. 32 w + 31, w = 0..3)
@@ -269,8 +271,9 @@ __global__ __launch_bounds__(kDkdvThreads, 1) void bwd_dkdv_kernel(BwdParams p) 
     if (partial && __ballot(w != 0u) == 0ull) return;
     const bool mixed = partial && __ballot(w != ~0u) != 0ull;
     const int rb = 32 * qh;
-    f32x16 sacc = f32x16{};
-    f32x16 dpacc = acc_rows(dlu + rb, g);  // -Delta: the chain ends at dP - Delta
+    // Chains start from -LSE / c and -Delta and end at S - LSE / c, dP - Delta.
+    f32x16 sacc = acc_rows(lu + rb, g);
+    f32x16 dpacc = acc_rows(dlu + rb, g);
     __builtin_amdgcn_s_setprio(1);  // MFMA runs at raised wave priority
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
@@ -286,13 +289,12 @@ __global__ __launch_bounds__(kDkdvThreads, 1) void bwd_dkdv_kernel(BwdParams p) 
     // the pair's sign-extended mask bit, after the exponential.  Only a
     // mixed block can hold a fully masked row (LSE = -inf), whose
     // exp2(+inf) is cleared the same way; every other row has a finite LSE.
-    const f32x16 lrow = acc_rows(lu + rb, g);
     if (mixed) {
-      keep_masked(sacc, w >> g, lrow, dpacc, c);
+      keep_masked(sacc, w >> g, dpacc, c);
     } else {
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        const float pv = fast_exp2(fmaf(sacc[i], c, -lrow[i]));
+        const float pv = fast_exp2(sacc[i] * c);
         sacc[i] = pv;                  // P
         dpacc[i] = pv * dpacc[i];      // dS
       }
@@ -328,14 +330,14 @@ __global__ __launch_bounds__(kDkdvThreads, 1) void bwd_dkdv_kernel(BwdParams p) 
     const bool partial = it < npart;
     // Query rows [q0, q0 + 64): their units have landed; the other half's
     // units are free again.
-    publish_delta();
+    publish_rows();
     dma_barrier();
     load_q_part(q_hi, lse_hi, h, q0 + 64);
     load_do_part(do_hi, dl_hi, h, q0 + 64);
     block(q_lo, do_lo, lse_lo, dl_lo, qh ? wb.y : wb.x, partial);
 
     // Query rows [q0 + 64, q0 + 128); the first half's units are free again.
-    publish_delta();
+    publish_rows();
     dma_barrier();
     if (++it == nq) { it = 0; ++hh; }
     uint4 wn = wb;
