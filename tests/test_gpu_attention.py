@@ -87,6 +87,15 @@ def test_gqa_and_batch_masks(gpu_device):
     _oracle_check(rows, 2, 4, 2, 384, 64, seed=4, device=gpu_device)
 
 
+def test_gqa_grouped_dispatch(gpu_device):
+    """Hkv * tiles a multiple of 8: the forward and dQ launches place each
+    KV head's query heads on one XCD (head_and_slot's grouped mapping);
+    batch 2 and G = 4 so every (head, tile) work-group is checked."""
+    rng = np.random.default_rng(21)
+    rows = [random_row(512, rng, words=1, uncovered=False, max_doc=200) for _ in range(2)]
+    _oracle_check(rows, 2, 8, 2, 512, 128, seed=21, device=gpu_device)
+
+
 def test_ragged_uncovered_tokens(gpu_device):
     rng = np.random.default_rng(12)
     rows = [random_row(333, rng, words=1, uncovered=True, max_doc=90)]
