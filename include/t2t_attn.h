@@ -148,7 +148,10 @@ int t2t_mask_meta(const int32_t *doc, const uint64_t *q_bits, const uint64_t *kv
  * natural-log LSE = lse2 * ln 2; fully masked rows give o = 0, lse2 = -inf.
  * Supported: dtype T2T_DTYPE_BF16 or T2T_DTYPE_F32 (q, k, v, o all of that
  * type; float32 is computed in float32 throughout), D in {64, 128},
- * Hq % Hkv == 0.
+ * Hq % Hkv == 0, and a positive finite normal scale (every attention entry
+ * point rejects other scales with T2T_EINVAL: the kernels fold the scale
+ * into -inf mask seeds and -LSE / scale row seeds; torch's flex_attention
+ * would also take zero or negative scales).
  */
 int t2t_attn_fwd(const t2t_tensor *q, const t2t_tensor *k, const t2t_tensor *v,
                  const t2t_tensor *o, float *lse2, int32_t B, int32_t Hq, int32_t Hkv,

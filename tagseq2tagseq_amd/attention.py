@@ -306,6 +306,8 @@ def flex_attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
     _, _, _, _, D = _validate(query, key, value, block_mask, enable_gqa)
     if scale is None:
         scale = 1.0 / math.sqrt(D)  # torch/nn/attention/flex_attention.py:1544
+    if not (math.isfinite(scale) and scale > 0.0):
+        raise ValueError(f"scale={scale!r}: the gfx950 kernels need a positive finite scale")
     if torch.compiler.is_compiling():
         # compiled graphs trace the custom op (schema + fake implementation)
         out, lse2 = masked_attention(query, key, value, block_mask.tables(), float(scale))

@@ -1,6 +1,7 @@
 // extern "C" boundary of libt2t_attn.so: argument validation, error
 // reporting and dispatch to the gfx950 kernels.  No allocation happens here.
 #include <algorithm>
+#include <cfloat>
 #include <cstdarg>
 #include <cstdio>
 #include <mutex>
@@ -75,6 +76,15 @@ t2t::MaskTables as_tables(const t2t_block_mask* m) {
   t.kv_bits_off = m->kv_bits_off; t.q_bits_slot = m->q_bits_slot;
   t.tile_bits = m->tile_bits;
   return t;
+}
+
+// The kernels fold the softmax scale into masked-score seeds (-inf) and the
+// backward into row seeds (-LSE / scale): a positive normal scale is required
+// (torch's flex_attention would also accept zero or negative scales).
+int check_scale(float scale) {
+  if (!(scale >= FLT_MIN && scale <= FLT_MAX))
+    return fail(T2T_EINVAL, "scale=%g must be a positive finite normal number", (double)scale);
+  return T2T_OK;
 }
 
 int check_dims(int B, int Hq, int Hkv, int T, int D, int dtype, bool f32_ok = false) {
@@ -159,6 +169,8 @@ int t2t_attn_fwd(const t2t_tensor* q, const t2t_tensor* k, const t2t_tensor* v,
                  void* stream) {
   int rc = check_dims(B, Hq, Hkv, T, D, dtype, true);
   if (rc) return rc;
+  rc = check_scale(scale);
+  if (rc) return rc;
   if (B == 0 || Hq == 0 || T == 0) return T2T_OK;
   const int es = dtype == T2T_DTYPE_F32 ? 4 : 2;
   if (!view_ok(q, T, D, es) || !view_ok(k, T, D, es) || !view_ok(v, T, D, es) ||
@@ -202,6 +214,8 @@ int t2t_attn_bwd_dkdv(const t2t_tensor* q, const t2t_tensor* k, const t2t_tensor
                       const t2t_block_mask* mask, void* stream) {
   int rc = check_dims(B, Hq, Hkv, T, D, dtype);
   if (rc) return rc;
+  rc = check_scale(scale);
+  if (rc) return rc;
   if (B == 0 || Hq == 0 || T == 0) return T2T_OK;
   if (!view_ok(q, T, D) || !view_ok(k, T, D) || !view_ok(v, T, D) || !view_ok(dout, T, D) || !view_ok(dk, T, D) ||
       !view_ok(dv, T, D))
@@ -224,6 +238,8 @@ int t2t_attn_bwd_dq(const t2t_tensor* q, const t2t_tensor* k, const t2t_tensor* 
                     const t2t_tensor* dq, int32_t B, int32_t Hq, int32_t Hkv, int32_t T,
                     int32_t D, int32_t dtype, float scale, const t2t_block_mask* mask, void* stream) {
   int rc = check_dims(B, Hq, Hkv, T, D, dtype);
+  if (rc) return rc;
+  rc = check_scale(scale);
   if (rc) return rc;
   if (B == 0 || Hq == 0 || T == 0) return T2T_OK;
   if (!view_ok(q, T, D) || !view_ok(k, T, D) || !view_ok(v, T, D) || !view_ok(dout, T, D) || !view_ok(dq, T, D))
@@ -249,6 +265,8 @@ int t2t_attn_bwd(const t2t_tensor* q, const t2t_tensor* k, const t2t_tensor* v,
                  void* stream) {
   // Validate every argument before launching anything.
   int rc = check_dims(B, Hq, Hkv, T, D, dtype, true);
+  if (rc) return rc;
+  rc = check_scale(scale);
   if (rc) return rc;
   if (B == 0 || Hq == 0 || T == 0) return T2T_OK;
   const int es = dtype == T2T_DTYPE_F32 ? 4 : 2;
@@ -320,6 +338,8 @@ int t2t_attn_bwd_noalloc(const t2t_tensor* q, const t2t_tensor* k, const t2t_ten
                          int32_t B, int32_t Hq, int32_t Hkv, int32_t T, int32_t D, int32_t dtype,
                          float scale, const t2t_block_mask* mask, void* stream) {
   int rc = check_dims(B, Hq, Hkv, T, D, dtype, true);
+  if (rc) return rc;
+  rc = check_scale(scale);
   if (rc) return rc;
   if (B == 0 || Hq == 0 || T == 0) return T2T_OK;
   const int64_t rows = (int64_t)B * Hq * T;
@@ -417,6 +437,7 @@ int t2t_attn_decode(const t2t_tensor* q, const t2t_tensor* k, const t2t_tensor* 
   if (D != 64 && D != 128) return fail(T2T_EUNSUPPORTED, "head dim %d (64 or 128)", D);
   if (words < 0 || words > T2T_MAX_WORDS)
     return fail(T2T_EUNSUPPORTED, "words=%d outside [0, %d]", words, T2T_MAX_WORDS);
+  if (int rc = check_scale(scale)) return rc;
   if (B == 0 || Hq == 0 || Tq == 0) return T2T_OK;
   if (Hkv == 0 || Hq % Hkv != 0)
     return fail(T2T_EINVAL, "Hq=%d is not a multiple of Hkv=%d", Hq, Hkv);

@@ -62,6 +62,32 @@ def test_fwd_rejects_bad_gqa_and_dtype():
 
 
 @no_gpu
+def test_attention_rejects_nonpositive_scales():
+    """Zero, negative, denormal, infinite and NaN scales are refused by every
+    attention entry point before any launch."""
+    v = _dummy_view()
+    m = _lib.T2TBlockMaskC()
+    lib = _lib.lib()
+    P = ctypes.c_void_p(0x1000)
+    for scale in (0.0, -0.125, 1e-40, float("inf"), float("nan")):
+        rc = lib.t2t_attn_fwd(*[ctypes.byref(v)] * 4, P, 1, 2, 2, 256, 128, 0, scale,
+                              ctypes.byref(m), None)
+        assert rc == -1 and "scale" in _err(), scale
+        rc = lib.t2t_attn_bwd(*[ctypes.byref(v)] * 5, P, P, *[ctypes.byref(v)] * 3,
+                              1, 2, 2, 256, 128, 0, scale, ctypes.byref(m), None)
+        assert rc == -1 and "scale" in _err(), scale
+        rc = lib.t2t_attn_bwd_dkdv(*[ctypes.byref(v)] * 4, P, P, ctypes.byref(v), ctypes.byref(v),
+                                   1, 2, 2, 256, 128, 0, scale, ctypes.byref(m), None)
+        assert rc == -1 and "scale" in _err(), scale
+        rc = lib.t2t_attn_bwd_dq(*[ctypes.byref(v)] * 4, P, P, ctypes.byref(v),
+                                 1, 2, 2, 256, 128, 0, scale, ctypes.byref(m), None)
+        assert rc == -1 and "scale" in _err(), scale
+        rc = lib.t2t_attn_bwd_noalloc(*[ctypes.byref(v)] * 5, P, *[ctypes.byref(v)] * 3,
+                                      1, 2, 2, 256, 128, 0, scale, ctypes.byref(m), None)
+        assert rc == -1 and "scale" in _err(), scale
+
+
+@no_gpu
 def test_float32_dtype_rules():
     """float32 (dtype 1) is accepted by t2t_attn_fwd / t2t_attn_bwd with
     4-byte-element alignment rules, and rejected by the separate phases."""
