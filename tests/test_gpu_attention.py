@@ -96,6 +96,36 @@ def test_gqa_grouped_dispatch(gpu_device):
     _oracle_check(rows, 2, 8, 2, 512, 128, seed=21, device=gpu_device)
 
 
+@pytest.mark.parametrize("scale", [0.02, 0.5])
+def test_explicit_scale(scale, gpu_device):
+    """A non-default scale reaches the forward's score scaling and the
+    backward's -LSE / scale row seeds; against the oracle at the same scale.
+    At 0.5 (5.7x the default for D = 128: scores of standard deviation ~5.7)
+    the softmax is sharp and the gradients span a wide range, so their bf16
+    rounding (of P, dS and the outputs) is bounded relative to each tensor's
+    largest entry; the element-wise bound holds at the small scale.
+    Non-positive scales are refused."""
+    rng = np.random.default_rng(31)
+    rows = [random_row(320, rng, words=1, uncovered=True, max_doc=100)]
+    bm = _mask_from_rows(rows, gpu_device)
+    q, k, v, do = _inputs(1, 4, 2, 320, 128, 31, gpu_device)
+    q.requires_grad_(True); k.requires_grad_(True); v.requires_grad_(True)
+    out, lse = flex_attention(q, k, v, block_mask=bm, scale=scale, enable_gqa=True, return_lse=True)
+    out.backward(do)
+    dense = np.stack([mo.dense_mask(*r) for r in rows])
+    qn, kn, vn, don = (t.detach().float().cpu().numpy() for t in (q, k, v, do))
+    o_ref, lse_ref = ao.attention_fwd(qn, kn, vn, dense, scale)
+    dq_ref, dk_ref, dv_ref = ao.attention_bwd(qn, kn, vn, o_ref, don, lse_ref, dense, scale)
+    assert_close(out.detach(), torch.from_numpy(o_ref), ATOL, RTOL, f"out scale {scale}")
+    assert_close(lse.detach(), torch.from_numpy(lse_ref), 1e-3, 1e-3, f"lse scale {scale}")
+    for name, got, ref in (("dq", q.grad, dq_ref), ("dk", k.grad, dk_ref), ("dv", v.grad, dv_ref)):
+        ref = torch.from_numpy(ref)
+        atol = ATOL if scale < 0.1 else ATOL * float(ref.abs().max())
+        assert_close(got, ref, atol, RTOL, f"{name} scale {scale}")
+    with pytest.raises(ValueError, match="scale"):
+        flex_attention(q, k, v, block_mask=bm, scale=-scale, enable_gqa=True)
+
+
 def test_ragged_uncovered_tokens(gpu_device):
     rng = np.random.default_rng(12)
     rows = [random_row(333, rng, words=1, uncovered=True, max_doc=90)]
