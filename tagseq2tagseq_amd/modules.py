@@ -1,6 +1,7 @@
 """Model modules around the masked attention, with the reference's
 constructors and call signatures, for the layer / backbone / training-step
-measurements (SURVEY config 5) and as the drop-in host of the attention.
+measurements (the 12-layer training-step workload) and as the drop-in host of
+the attention.
 
 Mirrors (reference file:line):
   * ``Layer`` -- model/modules/layer.py:11-35 (RMSNorm -> FlexSelfAttention ->

@@ -3,7 +3,7 @@
 Small cases: against the float64 CPU oracle (oracle/attn_oracle.py).
 Full-size configs: against a chunked fp32 torch reference on the GPU over a
 subset of heads.  bf16 tolerance 2e-2 (abs and rel), float32 1e-4: the
-north-star bounds.
+parity bounds set for this path.
 """
 import math
 
@@ -45,7 +45,7 @@ def _inputs(B, Hq, Hkv, T, D, seed, device, dtype=torch.bfloat16):
 
 def _oracle_check(rows_np, B, Hq, Hkv, T, D, seed, device, bwd=True, dtype=torch.bfloat16):
     """Kernels vs the float64 oracle on the same inputs: 2e-2 (abs and rel)
-    for bf16, 1e-4 for float32; LSE 1e-3 / 1e-4."""
+    for bf16, 1e-4 for float32 (the parity bounds set for this path); LSE 1e-3 / 1e-4."""
     tol, lse_tol = (ATOL, 1e-3) if dtype == torch.bfloat16 else (F32_TOL, F32_TOL)
     bm = _mask_from_rows(rows_np, device)
     q, k, v, do = _inputs(B, Hq, Hkv, T, D, seed, device, dtype)

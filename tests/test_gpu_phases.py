@@ -21,7 +21,7 @@ from tests.helpers import assert_close, random_row, to_dev_words
 
 pytestmark = pytest.mark.gpu
 
-TOL = 2e-2  # bf16 bound of the north star (abs and rel)
+TOL = 2e-2  # bf16 parity bound of this path (abs and rel)
 
 
 def _case(B, Hq, Hkv, T, D, words, seed, device):
