@@ -385,6 +385,18 @@ int t2t_first_input_diff(const int64_t *tokens_a, const int64_t *tokens_b, const
                          int64_t bits_stride_a, int64_t bits_stride_b, int32_t words, int32_t n,
                          int32_t *out, void *stream);
 
+/*
+ * Engine-clock probe.  No counterpart in the reference: measurement support
+ * for re-deriving the MFMA peak from the clock a box actually runs at.
+ * Enqueues one kernel in which every SIMD runs two waves of back-to-back
+ * v_mfma_f32_32x32x16_bf16 chains for `iters` iterations (1 .. 10^7) and one
+ * wave records its shader-cycle (s_memtime) and wall-clock (s_memrealtime)
+ * tick counts around its loop into out (uint64[2], device memory); wall_khz
+ * (host pointer) receives the wall-clock counter's rate.  Engine clock in MHz
+ * = out[0] / out[1] * wall_khz / 1000, read after the stream has finished.
+ */
+int t2t_clock_probe(uint64_t *out, int32_t iters, int32_t *wall_khz, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -51,6 +51,7 @@ _SIGS = {
     "t2t_mask_meta": ([_P, _P, _P, _I32, _I32, _I32, _P, _P, _P], ctypes.c_int),
     "t2t_attn_fwd": ([_P] * 5 + [_I32] * 6 + [ctypes.c_float, _P, _P], ctypes.c_int),
     "t2t_attn_bwd": ([_P] * 10 + [_I32] * 6 + [ctypes.c_float, _P, _P], ctypes.c_int),
+    "t2t_clock_probe": ([_P, _I32, _P, _P], ctypes.c_int),
     "t2t_attn_bwd_noalloc": ([_P] * 9 + [_I32] * 6 + [ctypes.c_float, _P, _P], ctypes.c_int),
     "t2t_attn_bwd_preprocess": ([_P] * 3 + [_I32] * 5 + [_P], ctypes.c_int),
     "t2t_attn_bwd_dkdv": ([_P] * 8 + [_I32] * 6 + [ctypes.c_float, _P, _P], ctypes.c_int),

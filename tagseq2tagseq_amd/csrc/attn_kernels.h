@@ -146,6 +146,11 @@ hipError_t launch_rows_qkv_rope(const __bf16* x, int64_t xs, int M, int K, const
                                 int max_pos, const TensorView& q, const TensorView& k,
                                 const TensorView& v, hipStream_t stream);
 
+// Engine-clock probe: out[0] / out[1] = shader cycles / wall-clock ticks of
+// one wave while every SIMD runs two waves of MFMA chains (iters iterations).
+hipError_t launch_clock_probe(uint64_t* out, int iters, hipStream_t stream);
+hipError_t wall_clock_khz(int* khz);
+
 // First position < n at which two copies of per-token inputs differ: lowers
 // *out (preset to n by the caller) to it (bits arrays [words][stride]).
 hipError_t launch_first_input_diff(const int64_t* ta, const int64_t* tb, const int32_t* da,

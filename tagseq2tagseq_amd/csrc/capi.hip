@@ -641,4 +641,15 @@ int t2t_first_input_diff(const int64_t* tokens_a, const int64_t* tokens_b, const
                     "t2t_first_input_diff launch");
 }
 
+int t2t_clock_probe(uint64_t* out, int32_t iters, int32_t* wall_khz, void* stream) {
+  if (!out || !wall_khz) return fail(T2T_EINVAL, "out or wall_khz is NULL");
+  if (iters < 1 || iters > 10000000) return fail(T2T_EINVAL, "iters=%d outside [1, 1e7]", iters);
+  int khz = 0;
+  hipError_t e = t2t::wall_clock_khz(&khz);
+  if (e != hipSuccess) return hip_status(e, "wall-clock rate query");
+  *wall_khz = khz;
+  return hip_status(t2t::launch_clock_probe(out, iters, static_cast<hipStream_t>(stream)),
+                    "t2t_clock_probe launch");
+}
+
 }  // extern "C"

@@ -88,6 +88,16 @@ def test_attention_rejects_nonpositive_scales():
 
 
 @no_gpu
+def test_clock_probe_argument_checks():
+    lib = _lib.lib()
+    khz = ctypes.c_int32(0)
+    assert lib.t2t_clock_probe(None, 100, ctypes.byref(khz), None) == -1
+    assert lib.t2t_clock_probe(ctypes.c_void_p(0x1000), 0, ctypes.byref(khz), None) == -1
+    assert "iters" in _err()
+    assert lib.t2t_clock_probe(ctypes.c_void_p(0x1000), 100, None, None) == -1
+
+
+@no_gpu
 def test_float32_dtype_rules():
     """float32 (dtype 1) is accepted by t2t_attn_fwd / t2t_attn_bwd with
     4-byte-element alignment rules, and rejected by the separate phases."""
