@@ -130,8 +130,9 @@ __global__ __launch_bounds__(kDkdvThreads, 1) void bwd_dkdv_kernel(BwdParams p) 
   constexpr int DT = D / 32;
   using U = UnitDma<D, kDkdvWaves>;
   constexpr int kUnit = U::kRows * pitch<D>();
-  __shared__ __bf16 k_s[kTile * pitch<D>()], v_s[kTile * pitch<D>()];
-  __shared__ __bf16 q_lo[kUnit], q_hi[kUnit], do_lo[kUnit], do_hi[kUnit];
+  // (16-byte aligned: the end of the kernel reuses them as float4 and row buffers)
+  __shared__ __align__(16) __bf16 k_s[kTile * pitch<D>()], v_s[kTile * pitch<D>()];
+  __shared__ __align__(16) __bf16 q_lo[kUnit], q_hi[kUnit], do_lo[kUnit], do_hi[kUnit];
   // LSE (log2 domain) and Delta of a half, slot 32 blk + m = query
   // 32 blk + tok_perm(m) (accumulator-row order).
   // (16-byte aligned: rows are read four at a time)
@@ -151,8 +152,6 @@ __global__ __launch_bounds__(kDkdvThreads, 1) void bwd_dkdv_kernel(BwdParams p) 
   const int kt = uniform(p.m.col_order[(size_t)mb * nt + blockIdx.y]);
   const int k0 = kt * kTile;
   const int kloc = 32 * kw + n;
-  const int key = k0 + kloc;
-  const bool kvalid = key < T;
   const float c = p.scale_log2;
 
   const size_t col = (size_t)mb * nt + kt;
@@ -353,41 +352,79 @@ __global__ __launch_bounds__(kDkdvThreads, 1) void bwd_dkdv_kernel(BwdParams p) 
     wb = wn;
   }
 
-  // Sum the two query blocks of each key group (qh = 1 hands its partials to
-  // qh = 0 through one of the Q / dO units, 16 KiB per wave), dK then dV.
-  float* red = reinterpret_cast<float*>(kw == 0 ? q_lo : kw == 1 ? q_hi : kw == 2 ? do_lo : do_hi);
-  static_assert(DT * 16 * 64 * sizeof(float) <= kUnit * sizeof(__bf16), "reduction fits a unit");
-  dma_barrier();
-  if (qh == 1) {
+  // Sum the two query blocks of each key group and store the tile's dK and
+  // dV.  The waves of a key group swap halves of their partials: (kw, 1)
+  // hands over its dK partial and (kw, 0) its dV partial (16 KiB per wave,
+  // one float4 per lane and step, in eight 16 KiB regions over the K / V
+  // tiles and the Q / dO units, all free after the loop), so (kw, 0) sums
+  // dK and (kw, 1) dV.  The sums go to LDS as bf16 rows of the tile (dK over
+  // the K tile, dV over the V tile, padded pitch), and all eight waves then
+  // store the 128 rows of each as whole rows, 16 bytes per lane -- instead
+  // of every lane writing 16-byte pieces of its own key's row.
+  {
+    static_assert(DT * 16 * 64 * sizeof(float) <= kUnit * sizeof(__bf16), "a region fits a unit");
+    static_assert(2 * DT * 16 * 64 * sizeof(float) <= kTile * pitch<D>() * sizeof(__bf16),
+                  "two regions fit a tile");
+    constexpr int kRegion = DT * 16 * 64;  // floats
+    auto region = [&](int r) {            // r < 4: dK partial of key group r, else dV of r - 4
+      float* base = r < 2 ? reinterpret_cast<float*>(k_s) + r * kRegion
+                  : r < 4 ? reinterpret_cast<float*>(v_s) + (r - 2) * kRegion
+                  : reinterpret_cast<float*>(r == 4 ? q_lo : r == 5 ? q_hi : r == 6 ? do_lo : do_hi);
+      return reinterpret_cast<float4*>(base);
+    };
+    dma_barrier();
+    {
+      float4* out = region(qh == 1 ? kw : 4 + kw);
+      const f32x16* give = qh == 1 ? dkacc : dvacc;
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
+      for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) red[(dt * 16 + i) * 64 + lane] = dkacc[dt][i];
-  }
-  __syncthreads();
-  if (qh == 0) {
+        for (int a = 0; a < 4; ++a)
+          out[(dt * 4 + a) * 64 + lane] = make_float4(give[dt][4 * a], give[dt][4 * a + 1],
+                                                      give[dt][4 * a + 2], give[dt][4 * a + 3]);
+    }
+    __syncthreads();
+    f32x16* mine = qh == 0 ? dkacc : dvacc;
+    {
+      const float4* in = region(qh == 0 ? kw : 4 + kw);
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
+      for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) dkacc[dt][i] += red[(dt * 16 + i) * 64 + lane];
-  }
-  __syncthreads();
-  if (qh == 1) {
+        for (int a = 0; a < 4; ++a) {
+          const float4 x = in[(dt * 4 + a) * 64 + lane];
+          mine[dt][4 * a] += x.x; mine[dt][4 * a + 1] += x.y;
+          mine[dt][4 * a + 2] += x.z; mine[dt][4 * a + 3] += x.w;
+        }
+    }
+    __syncthreads();
+    {
+      __bf16* rows = qh == 0 ? k_s : v_s;  // bf16 row kloc of dK (qh 0) or dV (qh 1)
+      const float mul = qh == 0 ? p.scale : 1.f;
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
+      for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) red[(dt * 16 + i) * 64 + lane] = dvacc[dt][i];
-  }
-  __syncthreads();
-  if (qh == 0 && kvalid) {
-    __bf16* dkp = p.dk + b * p.dk_sb + hk * p.dk_sh + (int64_t)key * p.dk_st;
-    __bf16* dvp = p.dv + b * p.dv_sb + hk * p.dv_sh + (int64_t)key * p.dv_st;
+        for (int a = 0; a < 4; ++a) {
+          bf16x4 w4;
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt) {
+          for (int e = 0; e < 4; ++e) w4[e] = (__bf16)(mine[dt][4 * a + e] * mul);
+          *reinterpret_cast<bf16x4*>(rows + kloc * pitch<D>() + 32 * dt + acc_row(4 * a, g)) = w4;
+        }
+    }
+    __syncthreads();
+    constexpr int kChunks = D / 8;  // 16-byte pieces per row
+    __bf16* dkp = p.dk + b * p.dk_sb + hk * p.dk_sh;
+    __bf16* dvp = p.dv + b * p.dv_sb + hk * p.dv_sh;
 #pragma unroll
-      for (int i = 0; i < 16; ++i) dvacc[dt][i] += red[(dt * 16 + i) * 64 + lane];
-      store_acc_t(dkp, dkacc[dt], 32 * dt, g, p.scale);
-      store_acc_t(dvp, dvacc[dt], 32 * dt, g, 1.f);
+    for (int j = 0; j < kTile * kChunks / kDkdvThreads; ++j) {
+      const int c = tid + kDkdvThreads * j;
+      const int r = c / kChunks, ch = c % kChunks;
+      if (k0 + r < T) {
+        const int64_t row = k0 + r;
+        *reinterpret_cast<uint4*>(dkp + row * p.dk_st + 8 * ch) =
+            *reinterpret_cast<const uint4*>(k_s + r * pitch<D>() + 8 * ch);
+        *reinterpret_cast<uint4*>(dvp + row * p.dv_st + 8 * ch) =
+            *reinterpret_cast<const uint4*>(v_s + r * pitch<D>() + 8 * ch);
+      }
     }
   }
 }
