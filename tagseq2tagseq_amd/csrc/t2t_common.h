@@ -116,6 +116,12 @@ __device__ __forceinline__ void unit_dma(__bf16* dst, __amdgpu_buffer_rsrc_t src
 // them, but the explicit form keeps the compiler from hoisting LDS reads
 // across it and documents what the pipeline relies on).
 __device__ __forceinline__ void dma_barrier() {
+  // The same wait as a builtin first: the compiler's wait-count tracking does
+  // not read inline assembly, and without it would still count the loads
+  // issued before the barrier as outstanding afterwards -- and place waits
+  // for them (with counts that can also cover the copies issued after the
+  // barrier) in front of the next compute.
+  __builtin_amdgcn_s_waitcnt(0);
   asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
