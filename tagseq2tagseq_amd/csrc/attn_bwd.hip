@@ -549,26 +549,38 @@ __global__ __launch_bounds__(kThreads, 2) void bwd_dq_kernel(BwdParams p) {
   // lane's bitmap word (all ones for full tiles).
   auto block = [&](const __bf16* ku, const __bf16* vu, uint32_t w, int j) {
     if (__ballot(w != 0u) == 0ull) return;
-    const bool mixed = __ballot(w != ~0u) != 0ull;
-    f32x16 sacc = mixed ? mask_bias(~(w >> g)) : f32x16{};
-    f32x16 dpacc = dseed;
-    __builtin_amdgcn_s_setprio(1);  // MFMA runs at raised wave priority
+    f32x16 sacc, dpacc;
+    // The score chain starts from the mask seed (mixed blocks) or from the
+    // MFMA's inline zero (no register initialisation): one copy of the run
+    // for each start.  MFMA runs at raised wave priority.
+    auto score_run = [&](auto seeded) __attribute__((always_inline)) {
+      __builtin_amdgcn_s_setprio(1);
 #pragma unroll
-    for (int s = 0; s < KS; ++s) {
-      const bf16x8 ka = lds_row8<D>(ku, 32 * j + tok_perm(n), 16 * s + 8 * g);
-      const bf16x8 va = lds_row8<D>(vu, 32 * j + tok_perm(n), 16 * s + 8 * g);
-      sacc = mfma32(ka, qf[s], sacc);
-      dpacc = mfma32(va, dof[s], dpacc);
-    }
-    // LDS reads four MFMAs ahead of their use.
-    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+      for (int s = 0; s < KS; ++s) {
+        const bf16x8 ka = lds_row8<D>(ku, 32 * j + tok_perm(n), 16 * s + 8 * g);
+        const bf16x8 va = lds_row8<D>(vu, 32 * j + tok_perm(n), 16 * s + 8 * g);
+        if (decltype(seeded)::value || s > 0)
+          sacc = mfma32(ka, qf[s], sacc);
+        else
+          sacc = mfma32(ka, qf[s], f32x16{});
+        dpacc = mfma32(va, dof[s], s > 0 ? dpacc : dseed);
+      }
+      // LDS reads four MFMAs ahead of their use.
+      __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
 #pragma unroll
-    for (int i = 0; i < 2 * KS - 4; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      for (int i = 0; i < 2 * KS - 4; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+      __builtin_amdgcn_s_setprio(0);
+    };
+    if (__ballot(w != ~0u) != 0ull) {
+      sacc = mask_bias(~(w >> g));
+      score_run(std::true_type{});
+    } else {
+      score_run(std::false_type{});
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
-    __builtin_amdgcn_s_setprio(0);
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       const float pv = fast_exp2(fmaf(sacc[i], c, neg_lse));

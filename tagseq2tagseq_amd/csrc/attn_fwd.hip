@@ -147,33 +147,41 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(FwdParams p)
                        bool partial) {
     if (partial && __ballot((w0 | w1) != 0u) == 0ull) return;
     f32x16 st[2];
+    // The two chains start from the mask seeds (mixed halves) or from the
+    // MFMA's inline zero (no register initialisation): one copy of the run
+    // for each start.  MFMA runs issue at raised wave priority, so that the
+    // wave sharing the SIMD fills the gaps with its softmax instead of
+    // competing for issue.
+    auto score_run = [&](auto seeded) __attribute__((always_inline)) {
+      __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+      for (int s = 0; s < KS; ++s)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const bf16x8 kf = lds_row8<D>(kt_lds, 32 * j + tok_perm(n), 16 * s + 8 * g);
+          if (decltype(seeded)::value || s > 0)
+            st[j] = mfma32(kf, qf[s], st[j]);
+          else
+            st[j] = mfma32(kf, qf[s], f32x16{});
+        }
+      // Issue the K reads a few MFMAs ahead of their use.
+      __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+      for (int i = 0; i < 2 * KS - 4; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+      __builtin_amdgcn_s_setprio(0);
+    };
     if (partial && __ballot((w0 & w1) != ~0u) != 0ull) {
       st[0] = mask_bias(~(w0 >> g));
       st[1] = mask_bias(~(w1 >> g));
+      score_run(std::true_type{});
     } else {
-      st[0] = f32x16{};
-      st[1] = f32x16{};
+      score_run(std::false_type{});
     }
-    // MFMA runs issue at raised wave priority, so that the wave sharing the
-    // SIMD fills the gaps with its softmax instead of competing for issue.
-    __builtin_amdgcn_s_setprio(1);
-#pragma unroll
-    for (int s = 0; s < KS; ++s)
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const bf16x8 kf = lds_row8<D>(kt_lds, 32 * j + tok_perm(n), 16 * s + 8 * g);
-        st[j] = mfma32(kf, qf[s], st[j]);
-      }
-    // Issue the K reads a few MFMAs ahead of their use.
-    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
-#pragma unroll
-    for (int i = 0; i < 2 * KS - 4; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-    }
-    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
 
-    __builtin_amdgcn_s_setprio(0);
     // Probabilities against the current reference max come first.  The
     // reference moves only when the row max exceeds it by 8 (log2 units),
     // i.e. when a probability would exceed 2^8; a lane whose probabilities

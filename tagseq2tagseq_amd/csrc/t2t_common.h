@@ -26,6 +26,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 namespace t2t {
 
 constexpr int kTile = 128;      // BlockMask tile edge (tokens)
