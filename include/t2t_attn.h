@@ -61,8 +61,11 @@ typedef struct t2t_tensor {
  * torch/nn/attention/flex_attention.py:586-657) with the head dimension
  * dropped: *_num int32[Bm][nt], *_idx int32[Bm][nt][nt].  The rest are this
  * library's additions:
- *   row_order / col_order int32[Bm][nt]: tile rows / columns by descending
- *       count of non-skip tiles (launch order for load balance);
+ *   row_order / col_order int32[Bm][nt]: launch orders -- tile rows /
+ *       columns by descending count of non-skip tiles taken in buckets of
+ *       two (count / 2), within a bucket rows by descending and columns by
+ *       ascending index (longest first for load balance, neighbours back to
+ *       back for cache reuse of the tiles they share);
  *   kv_bits_off int32[Bm][nt]: bitmap slot of the first partial tile of a
  *       row (the i-th partial tile of row r uses slot kv_bits_off[r] + i);
  *   q_bits_slot int32[Bm][nt][nt]: bitmap slot of the i-th partial tile of a

@@ -238,11 +238,16 @@ def _ordered(flags: torch.Tensor):
     return flags.sum(-1, dtype=torch.int32), key.argsort(-1).to(torch.int32)
 
 
-def _rank_desc(count: torch.Tensor) -> torch.Tensor:
-    """Indices by descending count, ties by higher index first (the launch
-    orders of the metadata pass)."""
+ORDER_BUCKET = 2  # non-skip tiles per launch-order bucket (mask_meta.hip)
+
+
+def _launch_order(count: torch.Tensor, index_desc: bool) -> torch.Tensor:
+    """Indices by descending count // ORDER_BUCKET, within a bucket by
+    descending (rows) or ascending (columns) index: the launch orders of the
+    metadata pass."""
     n = count.shape[-1]
-    key = count.to(torch.int64) * n + torch.arange(n, device=count.device)
+    idx = torch.arange(n, device=count.device)
+    key = (count.to(torch.int64) // ORDER_BUCKET) * n + (idx if index_desc else n - 1 - idx)
     return key.argsort(-1, descending=True).to(torch.int32)
 
 
@@ -297,8 +302,8 @@ def from_torch_block_mask(bm, tile_chunk: int = 256) -> T2TBlockMask:
     fkv_num, fkv_idx = _ordered(full)
     q_num, q_idx = _ordered(part.transpose(1, 2))
     fq_num, fq_idx = _ordered(full.transpose(1, 2))
-    row_order = _rank_desc(kv_num + fkv_num)
-    col_order = _rank_desc(q_num + fq_num)
+    row_order = _launch_order(kv_num + fkv_num, True)
+    col_order = _launch_order(q_num + fq_num, False)
     flat = kv_num.reshape(-1).to(torch.int64)
     kv_bits_off = (torch.cumsum(flat, 0) - flat).reshape(Bm, nt).to(torch.int32)
     # slot of partial tile (b, r, c): the row's first slot + its rank in the row

@@ -208,8 +208,13 @@ namespace {
 constexpr int kRankChunk = 512;
 
 // Launch orders of mask row b, by the whole work-group: rows / columns ranked
-// by descending non-skip tile count (ties: higher index first), the counts
-// staged through LDS in chunks.
+// by descending non-skip tile count in buckets of kOrderBucket tiles, rows of
+// one bucket by descending index and columns by ascending index -- longest
+// first for the load balance, and within a bucket neighbouring rows (which
+// mostly read the same K/V tiles) or columns back to back, so that a cache
+// serves the shared tiles.  The counts are staged through LDS in chunks.
+constexpr int kOrderBucket = 2;
+
 __device__ void rank_orders(const MaskOut& out, int b, int* rtot, int* ctot) {
   const int nt = out.nt, tid = threadIdx.x;
   const int32_t* rn = out.kv_num + (size_t)b * nt;
@@ -218,20 +223,21 @@ __device__ void rank_orders(const MaskOut& out, int b, int* rtot, int* ctot) {
   const int32_t* cf = out.full_q_num + (size_t)b * nt;
   for (int i0 = 0; i0 < nt; i0 += kThreads) {
     const int i = i0 + tid;
-    const int ri = i < nt ? rn[i] + rf[i] : 0, ci = i < nt ? cn[i] + cf[i] : 0;
+    const int ri = i < nt ? (rn[i] + rf[i]) / kOrderBucket : 0;
+    const int ci = i < nt ? (cn[i] + cf[i]) / kOrderBucket : 0;
     int rr = 0, rc = 0;
     for (int j0 = 0; j0 < nt; j0 += kRankChunk) {
       const int m = min(kRankChunk, nt - j0);
       __syncthreads();
       for (int j = tid; j < m; j += kThreads) {
-        rtot[j] = rn[j0 + j] + rf[j0 + j];
-        ctot[j] = cn[j0 + j] + cf[j0 + j];
+        rtot[j] = (rn[j0 + j] + rf[j0 + j]) / kOrderBucket;
+        ctot[j] = (cn[j0 + j] + cf[j0 + j]) / kOrderBucket;
       }
       __syncthreads();
       for (int j = 0; j < m; ++j) {
         const int rj = rtot[j], cj = ctot[j];
         rr += (rj > ri) || (rj == ri && j0 + j > i);
-        rc += (cj > ci) || (cj == ci && j0 + j > i);
+        rc += (cj > ci) || (cj == ci && j0 + j < i);
       }
     }
     if (i < nt) {

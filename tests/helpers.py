@@ -159,9 +159,13 @@ def _check_extras(bm, b, doc, qb, kb, label):
     bits = bm.tile_bits.cpu().numpy()
     assert sorted(row_order.tolist()) == list(range(nt)), f"{label}: row_order not a permutation"
     assert sorted(col_order.tolist()) == list(range(nt)), f"{label}: col_order not a permutation"
-    rc = (kv_num + full_num)[row_order]
-    cc = (q_num + q_full)[col_order]
-    assert (np.diff(rc) <= 0).all() and (np.diff(cc) <= 0).all(), f"{label}: orders not longest-first"
+    # launch orders: non-skip counts in buckets of two, longest first; within a
+    # bucket rows by descending index, columns by ascending index
+    idx = np.arange(nt)
+    exp_rows = np.lexsort((-idx, -((kv_num + full_num) // 2)))
+    exp_cols = np.lexsort((idx, -((q_num + q_full) // 2)))
+    np.testing.assert_array_equal(row_order, exp_rows, err_msg=f"{label}: row_order")
+    np.testing.assert_array_equal(col_order, exp_cols, err_msg=f"{label}: col_order")
     base = int(bm.kv_num_blocks[:b].sum().item())
     exp_off = base + np.concatenate([[0], np.cumsum(kv_num)[:-1]])
     np.testing.assert_array_equal(off, exp_off, err_msg=f"{label}: kv_bits_off")
