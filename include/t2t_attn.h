@@ -66,10 +66,12 @@ typedef struct t2t_tensor {
  *       two (count / 2), within a bucket rows by descending and columns by
  *       ascending index (longest first for load balance, neighbours back to
  *       back for cache reuse of the tiles they share);
- *   kv_bits_off int32[Bm][nt]: bitmap slot of the first partial tile of a
- *       row (the i-th partial tile of row r uses slot kv_bits_off[r] + i);
+ *   kv_bits_off int32[Bm][nt]: bitmap slots of a tile row: partial tile
+ *       (r, c) uses slot kv_bits_off[r] + c (t2t_mask_meta writes
+ *       b nt (nt + 1) / 2 + r (r + 1) / 2, the tile's position in the lower
+ *       triangle);
  *   q_bits_slot int32[Bm][nt][nt]: bitmap slot of the i-th partial tile of a
- *       column;
+ *       column (entries past q_num unspecified);
  *   tile_bits uint32[tile_bits_slots][2][128][4]: per partial tile, the
  *       allowed pairs as bits -- [0][q][w] bit j = allowed(q0 + q, k0 + 32 w + j),
  *       [1][k][w] bit j = allowed(q0 + 32 w + j, k0 + k);

@@ -304,18 +304,19 @@ def from_torch_block_mask(bm, tile_chunk: int = 256) -> T2TBlockMask:
     fq_num, fq_idx = _ordered(full.transpose(1, 2))
     row_order = _launch_order(kv_num + fkv_num, True)
     col_order = _launch_order(q_num + fq_num, False)
-    flat = kv_num.reshape(-1).to(torch.int64)
-    kv_bits_off = (torch.cumsum(flat, 0) - flat).reshape(Bm, nt).to(torch.int32)
-    # slot of partial tile (b, r, c): the row's first slot + its rank in the row
-    rank = torch.cumsum(part.to(torch.int32), -1) - 1
-    slot_grid = torch.where(part, kv_bits_off[:, :, None] + rank, torch.zeros_like(rank))
+    # bitmap slot of tile (b, r, c): b nt (nt + 1) / 2 + r (r + 1) / 2 + c, a
+    # fixed position in the lower triangle (the metadata pass's layout)
+    tri = nt * (nt + 1) // 2
+    kv_bits_off = (torch.arange(Bm, device=dev)[:, None] * tri
+                   + ar * (ar + 1) // 2).to(torch.int32)
+    slot_grid = kv_bits_off[:, :, None].to(torch.int64) + ar[None, None, :]
     q_bits_slot = torch.gather(slot_grid.transpose(1, 2), 2, q_idx.to(torch.int64))
     q_bits_slot = torch.where(ar[None, None, :] < q_num[:, :, None], q_bits_slot,
                               torch.zeros_like(q_bits_slot)).to(torch.int32)
-    # bitmaps of the partial tiles, in slot order (row-major enumeration)
+    # bitmaps of the partial tiles
     pb, pr, pc = part.nonzero(as_tuple=True)
     P = int(pb.numel())
-    tile_bits = torch.zeros((max(1, P), 2, TILE, 4), **i32)
+    tile_bits = torch.zeros((max(1, Bm * tri), 2, TILE, 4), **i32)
     t = torch.arange(TILE, device=dev)
     for s0 in range(0, P, tile_chunk):
         b_, r_, c_ = (x[s0:s0 + tile_chunk] for x in (pb, pr, pc))
@@ -325,8 +326,9 @@ def from_torch_block_mask(bm, tile_chunk: int = 256) -> T2TBlockMask:
         m = bm.mask_mod(b_[:, None, None], torch.zeros_like(b_)[:, None, None],
                         qpos.clamp(max=T - 1), kpos.clamp(max=T - 1))
         m = torch.as_tensor(m, device=dev).expand(ok.shape) & ok
-        tile_bits[s0:s0 + tile_chunk, 0] = _pack_bits(m)
-        tile_bits[s0:s0 + tile_chunk, 1] = _pack_bits(m.transpose(1, 2))
+        slots = slot_grid[b_, r_, c_]
+        tile_bits[slots, 0] = _pack_bits(m)
+        tile_bits[slots, 1] = _pack_bits(m.transpose(1, 2))
     out = T2TBlockMask(
         seq_len=T, doc_ids=torch.zeros((Bm, T), **i32),
         q_bits=torch.zeros((Bm, 0, T), dtype=torch.int64, device=dev),

@@ -148,7 +148,7 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_dq_f32_kernel(BwdF32Params p)
     const int kt = uniform(partial ? pidx[it] : fidx[it - npart]);
     uint4 wq = make_uint4(~0u, ~0u, ~0u, ~0u);
     if (partial)
-      wq = *reinterpret_cast<const uint4*>(bits_row + (size_t)it * kTileBitsWords + qloc * 4);
+      wq = *reinterpret_cast<const uint4*>(bits_row + (size_t)kt * kTileBitsWords + qloc * 4);
 #pragma unroll 1
     for (int j = 0; j < 4; ++j) {
       const uint32_t w = j == 0 ? wq.x : j == 1 ? wq.y : j == 2 ? wq.z : wq.w;

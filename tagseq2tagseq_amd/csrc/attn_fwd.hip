@@ -120,13 +120,14 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(FwdParams p)
     unit_dma<D>(kd, krs, koff, t0 * k_row2, wave, 0, dma_scratch);
     unit_dma<D>(vd, vrs, voff, t0 * v_row2, wave, 1, dma_scratch);
   };
-  // Row-major half (128 queries x 4 words) of tile `it`'s bitmap slot; each
-  // wave copies 1 KiB (waves w and w + 2 copy the same bytes).
-  // (Tiles without a bitmap, it >= npart, copy zeros.)
-  auto load_bits = [&](int it) {
+  // Row-major half (128 queries x 4 words) of the bitmap of iteration it
+  // (KV tile kt, slot kv_bits_off + kt); each wave copies 1 KiB (waves w and
+  // w + 2 copy the same bytes).  (Tiles without a bitmap, it >= npart, copy
+  // zeros.)
+  auto load_bits = [&](int it, int kt) {
     const bool has = it < npart;
     const auto rs = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint32_t*>(bits_row + (has ? (size_t)it * kTileBitsWords : 0)), 0,
+        const_cast<uint32_t*>(bits_row + (has ? (size_t)kt * kTileBitsWords : 0)), 0,
         has ? kTile * 16 : 0, 0x00020000);
     __builtin_amdgcn_raw_ptr_buffer_load_lds(
         rs, (__attribute__((address_space(3))) void*)(&bits_lds[it & 1][(wave & 1) * 256]), 16,
@@ -252,7 +253,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(FwdParams p)
   int k0_next = ntiles > 0 ? tile_of(0) * kTile : 0;
   if (ntiles > 0) {
     load_half(k_lo, v_lo, k0_next);
-    if (npart > 0) load_bits(0);
+    if (npart > 0) load_bits(0, k0_next / kTile);
   }
   for (int it = 0; it < ntiles; ++it) {
     const bool partial = it < npart;
@@ -274,7 +275,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(FwdParams p)
     }
     if (more) {
       load_half(k_lo, v_lo, k0_next);
-      load_bits(it + 1);
+      load_bits(it + 1, k0_next / kTile);
     }
     half_step(k_hi, v_hi, mbits.z, mbits.w, partial);
   }

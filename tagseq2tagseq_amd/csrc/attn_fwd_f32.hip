@@ -127,10 +127,11 @@ __global__ __launch_bounds__(kThreads, 1) void attn_fwd_f32_kernel(FwdF32Params 
     unit_dma<2 * D>(reinterpret_cast<__bf16*>(kd), krs, koff, t0 * k_row4, wave, 0, dma_scratch);
     unit_dma<2 * D>(reinterpret_cast<__bf16*>(vd), vrs, voff, t0 * v_row4, wave, 1, dma_scratch);
   };
-  auto load_bits = [&](int it) {
+  // bitmap of iteration it: KV tile kt, slot kv_bits_off + kt
+  auto load_bits = [&](int it, int kt) {
     const bool has = it < npart;
     const auto rs = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint32_t*>(bits_row + (has ? (size_t)it * kTileBitsWords : 0)), 0,
+        const_cast<uint32_t*>(bits_row + (has ? (size_t)kt * kTileBitsWords : 0)), 0,
         has ? kTile * 16 : 0, 0x00020000);
     __builtin_amdgcn_raw_ptr_buffer_load_lds(
         rs, (__attribute__((address_space(3))) void*)(&bits_lds[it & 1][(wave & 1) * 256]), 16,
@@ -209,7 +210,7 @@ __global__ __launch_bounds__(kThreads, 1) void attn_fwd_f32_kernel(FwdF32Params 
   int k0_next = ntiles > 0 ? tile_of(0) * kTile : 0;
   if (ntiles > 0) {
     load_half(k_lo, v_lo, k0_next);
-    if (npart > 0) load_bits(0);
+    if (npart > 0) load_bits(0, k0_next / kTile);
   }
   for (int it = 0; it < ntiles; ++it) {
     const bool partial = it < npart;
@@ -226,7 +227,7 @@ __global__ __launch_bounds__(kThreads, 1) void attn_fwd_f32_kernel(FwdF32Params 
       if (((it + 1) & 63) == 0) tiles_v = load_chunk((it + 1) >> 6);
       k0_next = tile_of(it + 1) * kTile;
       load_half(k_lo, v_lo, k0_next);
-      load_bits(it + 1);
+      load_bits(it + 1, k0_next / kTile);
     }
     half_step(k_hi, v_hi, mbits.z, mbits.w, partial);
   }

@@ -166,8 +166,8 @@ def _check_extras(bm, b, doc, qb, kb, label):
     exp_cols = np.lexsort((idx, -((q_num + q_full) // 2)))
     np.testing.assert_array_equal(row_order, exp_rows, err_msg=f"{label}: row_order")
     np.testing.assert_array_equal(col_order, exp_cols, err_msg=f"{label}: col_order")
-    base = int(bm.kv_num_blocks[:b].sum().item())
-    exp_off = base + np.concatenate([[0], np.cumsum(kv_num)[:-1]])
+    # bitmap slot of tile (b, r, c): its position in the lower triangle
+    exp_off = b * (nt * (nt + 1) // 2) + np.arange(nt) * (np.arange(nt) + 1) // 2
     np.testing.assert_array_equal(off, exp_off, err_msg=f"{label}: kv_bits_off")
     row_slot = {}
     pad = nt * 128 - T
@@ -178,7 +178,7 @@ def _check_extras(bm, b, doc, qb, kb, label):
         rows = np.pad(rows, ((0, 128 - rows.shape[0]), (0, pad)))
         for i in range(kv_num[qt]):
             kt = kv_idx[qt, i]
-            slot = off[qt] + i
+            slot = off[qt] + kt
             row_slot[(qt, kt)] = slot
             tile = rows[:, kt * 128:(kt + 1) * 128]
             np.testing.assert_array_equal(bits[slot, 0].view("<u4"), _pack_bits(tile),
