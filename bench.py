@@ -125,6 +125,23 @@ def time_launches(fn, reps: int) -> float:
     return start.elapsed_time(end) / reps
 
 
+def median_ms(fn, reps: int = 50, warmup: int = 10):
+    """(median, min, max) duration in ms of fn() over `reps` calls after
+    `warmup` discarded ones, each call bracketed by its own HIP events."""
+    for _ in range(warmup):
+        fn()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(reps)]
+    torch.cuda.synchronize()
+    for e0, e1 in evs:
+        e0.record()
+        fn()
+        e1.record()
+    torch.cuda.synchronize()
+    t = sorted(e0.elapsed_time(e1) for e0, e1 in evs)
+    return t[len(t) // 2], t[0], t[-1]
+
+
 def engine_clock(dev, iters: int = 40000, reps: int = 5):
     """Engine clock (MHz) while every SIMD runs MFMA chains (t2t_clock_probe:
     shader cycles over wall-clock ticks of one wave), median of `reps`
@@ -868,6 +885,16 @@ def main():
     t_dkdv = time_launches(ph.dkdv, args.reps)
     t_dq = time_launches(ph.dq_pass, args.reps)
     t_bwd = time_launches(ph.whole, args.reps)
+    # The measurement plan's form: medians of >= 50 timed calls after 10
+    # discarded ones, forward alone and forward + backward, on the prebuilt
+    # mask (the metadata pass is timed separately above).
+    fwd_med = median_ms(lambda: attn_fwd(q, k, v, bm, scale))
+
+    def fwd_bwd():
+        o_, l_ = attn_fwd(q, k, v, bm, scale)
+        return attn_bwd(q, k, v, o_, do, l_, bm, scale)
+
+    fb_med = median_ms(fwd_bwd)
 
     base = D * n_pairs * Hq
     kernels = {
@@ -945,6 +972,14 @@ def main():
         # The step's backward is t2t_attn_bwd: dQ computing Delta itself, then
         # dK/dV (bwd_delta above is the separate-phase entry point's launch).
         "attn_bwd_ms": {"t2t_attn_bwd (dQ+Delta, dK/dV)": round(t_bwd, 4)},
+        "median_of_50": {
+            "fwd_ms": [round(x, 4) for x in fwd_med],
+            "fwd_TFLOPs": round(4.0 * base / (fwd_med[0] * 1e-3) / 1e12, 2),
+            "fwd_bwd_ms": [round(x, 4) for x in fb_med],
+            "fwd_bwd_TFLOPs": round(useful_flops / (fb_med[0] * 1e-3) / 1e12, 2),
+            "method": "median, min, max of 50 calls after 10 warm-ups, each bracketed by HIP "
+                      "events; mask prebuilt; useful FLOPs 4 D N_pairs Hq (fwd), 14 D N_pairs Hq",
+        },
         "mask_meta": {"us": round(t_meta * 1e3, 2), "bytes": int(meta_bytes),
                       "GBps": round(meta_bytes / (t_meta * 1e-3) / 1e9, 2)},
         "token_inputs": {"us": round(t_tok * 1e3, 2), "bytes": int(tok_bytes),
