@@ -141,6 +141,10 @@ int t2t_mask_meta(const int32_t* doc, const uint64_t* q_bits, const uint64_t* kv
     return fail(T2T_EINVAL, "out describes Bm=%d nt=%d, expected Bm=%d nt=%d", out->mask_batch,
                 out->num_tiles, mask_batch, nt);
   const int64_t need = (int64_t)mask_batch * nt * (nt + 1) / 2;
+  // bitmap slots are indexed with int32 (kv_bits_off, q_bits_slot)
+  if (need > 0x7fffffffLL)
+    return fail(T2T_EUNSUPPORTED, "Bm=%d x %lld tiles exceed the int32 bitmap slot range",
+                mask_batch, (long long)nt * (nt + 1) / 2);
   if (out->tile_bits_slots < need)
     return fail(T2T_EINVAL, "tile_bits holds %lld slots, %lld needed",
                 (long long)out->tile_bits_slots, (long long)need);

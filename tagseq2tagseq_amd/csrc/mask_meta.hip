@@ -39,10 +39,10 @@ namespace {
 // Lower-triangle tile of linear index L (row-major over qt, kt <= qt).
 __device__ __forceinline__ void tri_tile(int L, int& qt, int& kt) {
   int r = (int)((sqrtf(8.f * (float)L + 1.f) - 1.f) * 0.5f);
-  while ((r + 1) * (r + 2) / 2 <= L) ++r;  // exact despite float rounding
-  while (r * (r + 1) / 2 > L) --r;
+  while ((int64_t)(r + 1) * (r + 2) / 2 <= L) ++r;  // exact despite float rounding
+  while ((int64_t)r * (r + 1) / 2 > L) --r;
   qt = r;
-  kt = L - r * (r + 1) / 2;
+  kt = L - (int)((int64_t)r * (r + 1) / 2);
 }
 
 // Signatures (doc id, grant words) of the 128 tokens of one tile side, in
@@ -122,8 +122,9 @@ __device__ __forceinline__ bool sigs_allowed(const TileSigs& q, int a, const Til
 
 // First bitmap slot of mask row b's tile row qt (slot of tile (qt, kt) =
 // this + kt).
+// (t2t_mask_meta keeps every slot index below 2^31.)
 __device__ __forceinline__ int tri_slot(int b, int nt, int qt) {
-  return b * (nt * (nt + 1) / 2) + qt * (qt + 1) / 2;
+  return (int)((int64_t)b * ((int64_t)nt * (nt + 1) / 2) + (int64_t)qt * (qt + 1) / 2);
 }
 
 // Compact one 0/1 row of `n` byte flags (flag = (cls == want)) into the
@@ -388,7 +389,7 @@ hipError_t launch_mask_meta(const int32_t* doc, const uint64_t* qbits, const uin
                             int T, int words, const MaskOut& out, hipStream_t stream) {
   const int nt = out.nt;
   if (nt == 0 || out.Bm == 0) return hipSuccess;
-  const dim3 tiles((unsigned)(nt * (nt + 1) / 2), out.Bm);
+  const dim3 tiles((unsigned)((int64_t)nt * (nt + 1) / 2), out.Bm);
   const int sig_bytes = sig_lds_bytes(words);
   hipLaunchKernelGGL(mask_classify_tiles, tiles, dim3(128), sig_bytes, stream, doc, qbits, kvbits,
                      T, words, out);

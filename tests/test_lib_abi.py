@@ -149,6 +149,12 @@ def test_mask_meta_argument_checks():
     rc = lib.t2t_mask_meta(ctypes.c_void_p(0x1000), None, None, 1, 256, 0, ctypes.c_void_p(0x1000),
                            ctypes.byref(out), None)
     assert rc == -1 and "nt=" in _err()
+    # bitmap slots are int32 indices: 65536 tiles a side need 2^31 + 2^15 slots
+    nt = 65536
+    out = _lib.T2TBlockMaskC(1, nt, tile_bits_slots=1 << 40)
+    rc = lib.t2t_mask_meta(ctypes.c_void_p(0x1000), None, None, 1, nt * 128, 0,
+                           ctypes.c_void_p(0x1000), ctypes.byref(out), None)
+    assert rc == -2 and "int32" in _err()
 
 
 def test_python_layer_refuses_cpu_tensors():
