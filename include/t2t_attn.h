@@ -137,7 +137,8 @@ int t2t_token_inputs(const int32_t *spans, const int32_t *n_spans, int32_t max_s
  * and CrossDocLinkMaskCreator.__call__ (model/graph_traversal/cross_doc_mask.py:359-366),
  * without materialising the [T, T] mask.
  * tile_class: int8[Bm][nt][nt] out.  out->mask_batch / num_tiles must equal
- * mask_batch / ceil(T / 128).
+ * mask_batch / ceil(T / 128); mask_batch * nt (nt + 1) / 2 bitmap slots
+ * must fit int32 (T2T_EUNSUPPORTED otherwise).
  */
 int t2t_mask_meta(const int32_t *doc, const uint64_t *q_bits, const uint64_t *kv_bits,
                   int32_t mask_batch, int32_t T, int32_t words, int8_t *tile_class,
