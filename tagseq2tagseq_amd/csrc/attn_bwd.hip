@@ -283,6 +283,18 @@ __global__ __launch_bounds__(kDkdvThreads, 1) void bwd_dkdv_kernel(BwdParams p) 
       sacc = mfma32(qa, kb, sacc);
       dpacc = mfma32(da, vb, dpacc);
     }
+    if constexpr (D == 64) {
+      // The seeds and the operand reads of the first two MFMAs first, then
+      // each MFMA followed by the reads of the one two ahead (3 % faster at
+      // D = 64; at D = 128 the compiler's own order is faster).
+      __builtin_amdgcn_sched_group_barrier(0x100, 12, 0);
+#pragma unroll
+      for (int i = 0; i < 2 * KS - 2; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+    }
     __builtin_amdgcn_s_setprio(0);
     // Masked pairs of a mixed block: P is cleared by and-ing its bits with
     // the pair's sign-extended mask bit, after the exponential.  Only a
@@ -311,6 +323,16 @@ __global__ __launch_bounds__(kDkdvThreads, 1) void bwd_dkdv_kernel(BwdParams p) 
         dvacc[dt] = mfma32(doa, pb, dvacc[dt]);
         dkacc[dt] = mfma32(qa, sb, dkacc[dt]);
       }
+    }
+    if constexpr (D == 64) {
+      // transpose reads one MFMA ahead
+      __builtin_amdgcn_sched_group_barrier(0x100, 4, 1);
+#pragma unroll
+      for (int i = 0; i < 4 * DT - 2; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 1);
     }
     __builtin_amdgcn_s_setprio(0);
   };
