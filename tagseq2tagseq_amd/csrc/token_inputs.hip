@@ -13,9 +13,11 @@
 // (q_bits[t] = links[span(t)], kv_bits[t] = 1 << span(t)).
 //
 // One thread per (batch row, token): the row's spans and grants are staged
-// through LDS in chunks and scanned in order, so the result follows the
-// reference's sequential semantics for any span / grant list (overlapping or
-// unsorted included).
+// through LDS in chunks of 256; each wave marks which of its 64 entries touch
+// the work-group's 256 tokens (a ballot), and every thread then walks only the
+// marked entries, in list order, so the result follows the reference's
+// sequential semantics for any span / grant list (overlapping or unsorted
+// included) while a token reads a handful of entries instead of the whole list.
 #include "attn_kernels.h"
 
 namespace t2t {
@@ -38,10 +40,23 @@ struct TokenArgs {
   uint64_t* kv_bits;         // [B][words][T]
 };
 
+constexpr int kTokWaves = kTokThreads / 64;
+
+// Marks, per wave, the staged entries for which `hit` holds (lane i of wave w
+// for entry 64 w + i); returns after every thread can read the masks.
+__device__ __forceinline__ void mark_entries(bool hit, uint64_t* marks) {
+  const uint64_t m = __ballot(hit);
+  if ((threadIdx.x & 63) == 0) marks[threadIdx.x >> 6] = m;
+  __syncthreads();
+}
+
 __global__ __launch_bounds__(kTokThreads) void token_inputs_kernel(TokenArgs a) {
   __shared__ int32_t stage[kTokThreads * 5];
+  __shared__ uint64_t marks[kTokWaves];
   const int b = blockIdx.y;
-  const int t = blockIdx.x * kTokThreads + threadIdx.x;
+  const int t0 = blockIdx.x * kTokThreads;
+  const int t = t0 + threadIdx.x;
+  const int t1 = min(a.T, t0 + kTokThreads);  // this work-group's tokens: [t0, t1)
   // Counts come from device memory: clamp them to the declared capacities.
   const int ns = max(0, min(a.n_spans[b], a.max_spans));
 
@@ -50,17 +65,23 @@ __global__ __launch_bounds__(kTokThreads) void token_inputs_kernel(TokenArgs a) 
   for (int base = 0; base < ns; base += kTokThreads) {
     const int cnt = min(kTokThreads, ns - base);
     __syncthreads();
+    bool hit = false;
     if ((int)threadIdx.x < cnt) {
       const int32_t* s = a.spans + ((size_t)b * a.max_spans + base + threadIdx.x) * 3;
-      stage[3 * threadIdx.x + 0] = s[0];
-      stage[3 * threadIdx.x + 1] = s[1];
+      const int s0 = s[0], s1 = s[1];
+      stage[3 * threadIdx.x + 0] = s0;
+      stage[3 * threadIdx.x + 1] = s1;
       stage[3 * threadIdx.x + 2] = s[2];
+      hit = s0 < t1 && s1 > t0;
     }
-    __syncthreads();
-    for (int i = 0; i < cnt; ++i) {
-      if (stage[3 * i] <= t && t < stage[3 * i + 1]) {
-        span = base + i;
-        doc_id = stage[3 * i + 2];
+    mark_entries(hit, marks);
+    for (int w = 0; w < kTokWaves; ++w) {
+      for (uint64_t m = marks[w]; m; m &= m - 1) {
+        const int i = 64 * w + __ffsll((long long)m) - 1;
+        if (stage[3 * i] <= t && t < stage[3 * i + 1]) {
+          span = base + i;
+          doc_id = stage[3 * i + 2];
+        }
       }
     }
   }
@@ -82,22 +103,28 @@ __global__ __launch_bounds__(kTokThreads) void token_inputs_kernel(TokenArgs a) 
   for (int base = 0; base < ng; base += kTokThreads) {
     const int cnt = min(kTokThreads, ng - base);
     __syncthreads();
+    bool hit = false;
     if ((int)threadIdx.x < cnt) {
       const int32_t* g = a.grants + ((size_t)b * a.max_grants + base + threadIdx.x) * 5;
+      int e5[5];
 #pragma unroll
-      for (int e = 0; e < 5; ++e) stage[5 * threadIdx.x + e] = g[e];
+      for (int e = 0; e < 5; ++e) stage[5 * threadIdx.x + e] = e5[e] = g[e];
+      hit = (e5[1] < t1 && e5[2] > t0) || (e5[3] < t1 && e5[4] > t0);
     }
-    __syncthreads();
-    for (int i = 0; i < cnt; ++i) {
-      const int bit = stage[5 * i];
-      const uint64_t m = 1ull << (bit & 63);
-      const bool inq = stage[5 * i + 1] <= t && t < stage[5 * i + 2];
-      const bool ink = stage[5 * i + 3] <= t && t < stage[5 * i + 4];
+    mark_entries(hit, marks);
+    for (int w = 0; w < kTokWaves; ++w) {
+      for (uint64_t mk = marks[w]; mk; mk &= mk - 1) {
+        const int i = 64 * w + __ffsll((long long)mk) - 1;
+        const int bit = stage[5 * i];
+        const uint64_t m = 1ull << (bit & 63);
+        const bool inq = stage[5 * i + 1] <= t && t < stage[5 * i + 2];
+        const bool ink = stage[5 * i + 3] <= t && t < stage[5 * i + 4];
 #pragma unroll
-      for (int w = 0; w < kMaxWords; ++w) {
-        if (w == (bit >> 6)) {
-          if (inq) qw[w] |= m;
-          if (ink) kw[w] |= m;
+        for (int w2 = 0; w2 < kMaxWords; ++w2) {
+          if (w2 == (bit >> 6)) {
+            if (inq) qw[w2] |= m;
+            if (ink) kw[w2] |= m;
+          }
         }
       }
     }
