@@ -27,9 +27,12 @@
 // so no launch waits on a single work-group.  The bitmap of tile (b, qt, kt) lives in slot
 // b * nt (nt + 1) / 2 + qt (qt + 1) / 2 + kt (a fixed position in the lower
 // triangle), so no work-group has to count the partial tiles before its own.
-// Every work-group first copies the signatures (doc id, grant words) of its
-// tokens into LDS with one load per token and word, and finds the runs and
-// evaluates the predicate from there.
+// The runs are found in registers: each lane loads the signatures (doc id,
+// grant words) of its tokens and of the tokens just before them, a ballot of
+// "differs from the previous token" marks the run starts of 128 tokens as a
+// 128-bit mask, and the signature of a run is read at its first token (a
+// cached load); no work-group stages signatures in LDS or waits at a barrier
+// for them.
 #include "attn_kernels.h"
 
 namespace t2t {
@@ -45,41 +48,44 @@ __device__ __forceinline__ void tri_tile(int L, int& qt, int& kt) {
   kt = L - (int)((int64_t)r * (r + 1) / 2);
 }
 
-// Signatures (doc id, grant words) of the 128 tokens of one tile side, in
-// dynamic LDS: doc[i], bits[w * 128 + i].
-struct TileSigs {
-  int32_t* doc;
-  uint64_t* bits;
+// A token's signature: document id and grant words (zeros past T).  KW is
+// the compile-time bound on the words (registers are held for KW of them);
+// the `words` arguments below give how many are real (words <= KW).
+template <int KW>
+struct Sig {
+  int32_t doc;
+  uint64_t w[KW > 0 ? KW : 1];
 };
 
-// Bytes of dynamic LDS for the query and key signatures of one tile.
-__host__ __device__ constexpr int sig_lds_bytes(int words) {
-  return 2 * kTile * (int)(sizeof(int32_t) + words * sizeof(uint64_t));
+template <int KW>
+__device__ __forceinline__ Sig<KW> load_sig(const int32_t* doc, const uint64_t* bits, int words,
+                                            int T, int t) {
+  Sig<KW> g;
+  const bool in = t < T;
+  g.doc = in ? doc[t] : 0;
+#pragma unroll
+  for (int w = 0; w < KW; ++w) g.w[w] = (in && w < words) ? bits[(size_t)w * T + t] : 0ull;
+  return g;
 }
 
-// The query-side and key-side views of that LDS (bits first: 8-byte aligned).
-__device__ __forceinline__ void sig_views(unsigned char* lds, int words, TileSigs& q,
-                                          TileSigs& k) {
-  q.bits = reinterpret_cast<uint64_t*>(lds);
-  k.bits = q.bits + words * kTile;
-  q.doc = reinterpret_cast<int32_t*>(k.bits + words * kTile);
-  k.doc = q.doc + kTile;
+template <int KW>
+__device__ __forceinline__ bool sig_eq(const Sig<KW>& a, const Sig<KW>& b, int words) {
+  bool eq = a.doc == b.doc;
+#pragma unroll
+  for (int w = 0; w < KW; ++w)
+    if (w < words) eq = eq && a.w[w] == b.w[w];
+  return eq;
 }
 
-// Thread `i` (< 128) copies the signature of token base + i (zeros past T).
-__device__ __forceinline__ void load_sigs(const TileSigs& s, const int32_t* doc,
-                                          const uint64_t* bits, int words, int T, int base,
-                                          int i) {
-  const int t = base + i;
-  s.doc[i] = t < T ? doc[t] : 0;
-  for (int w = 0; w < words; ++w) s.bits[w * kTile + i] = t < T ? bits[(size_t)w * T + t] : 0ull;
-}
-
-__device__ __forceinline__ bool sigs_eq(const TileSigs& s, int a, int b, int words) {
-  if (s.doc[a] != s.doc[b]) return false;
-  for (int w = 0; w < words; ++w)
-    if (s.bits[w * kTile + a] != s.bits[w * kTile + b]) return false;
-  return true;
+// The non-causal part of the predicate for a query-side signature q and a
+// key-side signature k: same document, or a shared grant bit.
+template <int KW>
+__device__ __forceinline__ bool sig_allowed(const Sig<KW>& q, const Sig<KW>& k, int words) {
+  bool ok = q.doc == k.doc;
+#pragma unroll
+  for (int w = 0; w < KW; ++w)
+    if (w < words) ok = ok || (q.w[w] & k.w[w]) != 0ull;
+  return ok;
 }
 
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
@@ -89,35 +95,115 @@ __device__ __forceinline__ int lanes_below(uint64_t mask) {
                                    __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0));
 }
 
-// One wave over the LDS signatures of one tile side (the first nvalid tokens
-// are real): writes the start offsets of runs of identical signatures into
-// starts[], terminated by starts[n] = nvalid; returns n.
-__device__ int wave_runs(const TileSigs& s, int words, int nvalid, int* starts) {
-  const int lane = lane_id();
-  int flag[2];
+// Lane src's signature, fetched by every lane (src may differ per lane).
+template <int KW>
+__device__ __forceinline__ Sig<KW> shfl_sig(const Sig<KW>& g, int src, int words) {
+  Sig<KW> r;
+  r.doc = __shfl(g.doc, src, 64);
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const int t = lane + 64 * h;
-    flag[h] = t < nvalid && (t == 0 || !sigs_eq(s, t, t - 1, words));
+  for (int w = 0; w < KW; ++w) {
+    r.w[w] = 0ull;
+    if (w < words) {
+      const uint32_t lo = (uint32_t)__shfl((int)(uint32_t)g.w[w], src, 64);
+      const uint32_t hi = (uint32_t)__shfl((int)(uint32_t)(g.w[w] >> 32), src, 64);
+      r.w[w] = ((uint64_t)hi << 32) | lo;
+    }
   }
-  const uint64_t m0 = __ballot(flag[0]);
-  const uint64_t m1 = __ballot(flag[1]);
-  const int n0 = __popcll(m0);
-  if (flag[0]) starts[lanes_below(m0)] = lane;
-  if (flag[1]) starts[n0 + lanes_below(m1)] = lane + 64;
-  const int n = n0 + __popcll(m1);
-  if (lane == 0) starts[n] = nvalid;
-  return n;
+  return r;
 }
 
-// The non-causal part of the predicate for query-side token a and key-side
-// token c of a tile: same document, or a shared grant bit.
-__device__ __forceinline__ bool sigs_allowed(const TileSigs& q, int a, const TileSigs& k, int c,
-                                             int words) {
-  if (q.doc[a] == k.doc[c]) return true;
-  for (int w = 0; w < words; ++w)
-    if (q.bits[w * kTile + a] & k.bits[w * kTile + c]) return true;
-  return false;
+// Lane src's signature (src the same for every lane).
+template <int KW>
+__device__ __forceinline__ Sig<KW> readlane_sig(const Sig<KW>& g, int src, int words) {
+  Sig<KW> r;
+  r.doc = __builtin_amdgcn_readlane(g.doc, src);
+#pragma unroll
+  for (int w = 0; w < KW; ++w) {
+    r.w[w] = 0ull;
+    if (w < words) {
+      const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)g.w[w], src);
+      const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(g.w[w] >> 32), src);
+      r.w[w] = ((uint64_t)hi << 32) | lo;
+    }
+  }
+  return r;
+}
+
+// The 128 tokens base .. base + 127 of one tile side (the first nvalid are
+// real), held by one wave: lane l holds tokens base + l (sig[0]) and
+// base + 64 + l (sig[1]).  Bit i of the 128-bit run mask (m[0] bits 0-63,
+// m[1] bits 64-127) is set iff token base + i starts a run of identical
+// signatures.
+template <int KW>
+struct TileSide {
+  Sig<KW> sig[2];
+  uint64_t m[2];
+};
+
+template <int KW>
+__device__ __forceinline__ TileSide<KW> wave_tile_side(const int32_t* doc, const uint64_t* bits,
+                                                       int words, int T, int base, int nvalid) {
+  const int lane = lane_id();
+  TileSide<KW> s;
+  s.sig[0] = load_sig<KW>(doc, bits, words, T, base + lane);
+  s.sig[1] = load_sig<KW>(doc, bits, words, T, base + 64 + lane);
+  // predecessor of each token: lane - 1 of the same half; lane 0 of the
+  // second half takes lane 63 of the first
+  const int up = (lane + 63) & 63;
+  const Sig<KW> p0 = shfl_sig(s.sig[0], up, words);
+  const Sig<KW> t1 = shfl_sig(s.sig[1], up, words);
+  const Sig<KW> p1 = lane == 0 ? p0 : t1;
+  const bool f0 = lane < nvalid && (lane == 0 || !sig_eq(s.sig[0], p0, words));
+  const bool f1 = 64 + lane < nvalid && !sig_eq(s.sig[1], p1, words);
+  s.m[0] = __ballot(f0);
+  s.m[1] = __ballot(f1);
+  return s;
+}
+
+// The signature of token i of the side, for every lane's own i.
+template <int KW>
+__device__ __forceinline__ Sig<KW> side_sig(const TileSide<KW>& s, int i, int words) {
+  const Sig<KW> lo = shfl_sig(s.sig[0], i & 63, words);
+  const Sig<KW> hi = shfl_sig(s.sig[1], i & 63, words);
+  return i < 64 ? lo : hi;
+}
+
+// The run starts as a mask pair, for the helpers below.
+struct RunMask {
+  uint64_t m[2];
+};
+
+template <int KW>
+__device__ __forceinline__ RunMask run_mask(const TileSide<KW>& s) {
+  return RunMask{{s.m[0], s.m[1]}};
+}
+
+__device__ __forceinline__ int run_count(const RunMask& r) {
+  return __popcll(r.m[0]) + __popcll(r.m[1]);
+}
+
+// Position of the n-th (0-based) run start, or `none` when there are n or
+// fewer starts (the end of the last run).
+__device__ __forceinline__ int nth_start(const RunMask& r, int n, int none) {
+  const int c0 = __popcll(r.m[0]);
+  uint64_t m = r.m[0];
+  int pos = 0;
+  if (n >= c0) {
+    m = r.m[1];
+    pos = 64;
+    n -= c0;
+  }
+  if (n >= __popcll(m)) return none;
+#pragma unroll
+  for (int width = 32; width >= 1; width >>= 1) {
+    const int c = __popcll(m & ((1ull << width) - 1ull));
+    if (n >= c) {
+      n -= c;
+      m >>= width;
+      pos += width;
+    }
+  }
+  return pos;
 }
 
 // First bitmap slot of mask row b's tile row qt (slot of tile (qt, kt) =
@@ -162,64 +248,57 @@ __device__ void wave_ordered(const int8_t* cls, int stride, int n, int8_t want,
 
 }  // namespace
 
-// (1) grid (nt (nt + 1) / 2, Bm); block 128: one work-group decides one tile
-// of the lower triangle (kt <= qt) and writes its mirror above the diagonal
-// as skip (every pair there has kv > q).  Thread i copies the signatures of
-// query q0 + i and key k0 + i; waves 0 and 1 then find the query and key runs
-// side by side, and wave 0 evaluates the run pairs.
-__global__ __launch_bounds__(128) void mask_classify_tiles(
+// (1) grid (ceil(nt (nt + 1) / 2 / 4), Bm); block 256: each wave decides one
+// tile of the lower triangle (kt <= qt; linear index 4 x + wave, row-major)
+// and writes its mirror above the diagonal as skip (every pair there has
+// kv > q).  The wave finds the query and key run starts and evaluates the
+// run pairs, 64 at a time, stopping once the tile is known to be partial.
+constexpr int kClassifyWaves = kThreads / 64;
+
+template <int KW>
+__global__ __launch_bounds__(kThreads) void mask_classify_tiles(
     const int32_t* __restrict__ doc_all, const uint64_t* __restrict__ qbits_all,
     const uint64_t* __restrict__ kvbits_all, int T, int words, MaskOut out) {
-  extern __shared__ __align__(16) unsigned char sig_lds[];
-  __shared__ int q_starts[kTile + 1], kv_starts[kTile + 1];
-  __shared__ int n_qr, n_kr;
-  TileSigs qs, ks;
-  sig_views(sig_lds, words, qs, ks);
   const int nt = out.nt;
   const int b = blockIdx.y;
+  const int64_t L = (int64_t)blockIdx.x * kClassifyWaves + (threadIdx.x >> 6);
+  if (L >= (int64_t)nt * (nt + 1) / 2) return;
   int qt, kt;
-  tri_tile(blockIdx.x, qt, kt);
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  int8_t* dst = out.tile_class + ((size_t)b * nt + qt) * nt + kt;
-  if (tid == 0 && kt < qt) out.tile_class[((size_t)b * nt + kt) * nt + qt] = kSkip;
+  tri_tile((int)L, qt, kt);
+  const int lane = lane_id();
+  if (lane == 0 && kt < qt) out.tile_class[((size_t)b * nt + kt) * nt + qt] = kSkip;
   const int32_t* doc = doc_all + (size_t)b * T;
+  const uint64_t* qbits = qbits_all + (size_t)b * words * T;
+  const uint64_t* kbits = kvbits_all + (size_t)b * words * T;
   const int q0 = qt * kTile, k0 = kt * kTile;
   const int qvalid = min(kTile, T - q0), kvalid = min(kTile, T - k0);
-  load_sigs(qs, doc, qbits_all + (size_t)b * words * T, words, T, q0, tid);
-  load_sigs(ks, doc, kvbits_all + (size_t)b * words * T, words, T, k0, tid);
-  __syncthreads();
-  if (wave == 0) {
-    const int n = wave_runs(qs, words, qvalid, q_starts);
-    if (lane == 0) n_qr = n;
-  } else {
-    const int n = wave_runs(ks, words, kvalid, kv_starts);
-    if (lane == 0) n_kr = n;
-  }
-  __syncthreads();
-  if (wave != 0) return;
-  const int nqr = n_qr, nkr = n_kr;
+  const TileSide<KW> qs = wave_tile_side<KW>(doc, qbits, words, T, q0, qvalid);
+  const TileSide<KW> ks = wave_tile_side<KW>(doc, kbits, words, T, k0, kvalid);
+  const RunMask qr = run_mask(qs), kr = run_mask(ks);
+  const int nqr = run_count(qr), nkr = run_count(kr);
   // Padding rows/columns are False pairs: such a tile can never be full.
   bool any_true = false;
   bool any_false = (qvalid < kTile) || (kvalid < kTile);
   const int npairs = nqr * nkr;
   for (int p0 = 0; p0 < npairs; p0 += 64) {
     const int p = p0 + lane;
-    bool t = false, f = false;
-    if (p < npairs) {
-      const int r = p / nkr, s = p - r * nkr;
-      const int qa = q_starts[r], qb = q_starts[r + 1];
-      const int ka = kv_starts[s], kb = kv_starts[s + 1];
-      const bool v = sigs_allowed(qs, qa, ks, ka, words);
-      const bool exists_ge = (q0 + qb - 1) >= (k0 + ka);  // some pair with q >= kv
-      const bool exists_lt = (q0 + qa) < (k0 + kb - 1);   // some pair with q < kv
-      t = v && exists_ge;
-      f = !v || exists_lt;
-    }
+    const int r = min(p, npairs - 1) / nkr, c = min(p, npairs - 1) - r * nkr;
+    const int qa = nth_start(qr, r, 0), qb = nth_start(qr, r + 1, qvalid);
+    const int ka = nth_start(kr, c, 0), kb = nth_start(kr, c + 1, kvalid);
+    // every lane takes part in the shuffles (lanes past the last pair
+    // repeat it)
+    const bool v = sig_allowed(side_sig(qs, qa, words), side_sig(ks, ka, words), words);
+    const bool exists_ge = (q0 + qb - 1) >= (k0 + ka);  // some pair with q >= kv
+    const bool exists_lt = (q0 + qa) < (k0 + kb - 1);   // some pair with q < kv
+    const bool t = v && exists_ge;
+    const bool f = !v || exists_lt;
     any_true = any_true || (__ballot(t) != 0);
     any_false = any_false || (__ballot(f) != 0);
     if (any_true && any_false) break;
   }
-  if (lane == 0) *dst = any_true ? (any_false ? kPartial : kFull) : kSkip;
+  if (lane == 0)
+    out.tile_class[((size_t)b * nt + qt) * nt + kt] =
+        any_true ? (any_false ? kPartial : kFull) : kSkip;
 }
 
 // (2) grid (nt, Bm); block 256.  Wave 0/1: partial / full list of row x
@@ -311,77 +390,67 @@ __device__ __forceinline__ void set_bit_range(uint32_t acc[4], int lo, int hi) {
 // (3) grid (nt (nt + 1) / 2, Bm); block 256.  For a partial tile of the lower
 // triangle: both bitmap orientations, into slot tri_slot(b, nt, qt) + kt.
 // Work-group (qt, 0) also ranks row qt and column qt for the launch orders.
-// Threads 0..127 copy the query signatures, 128..255 the key signatures;
-// waves 0 and 1 find the runs.  A row of the bitmap is built run by run:
-// within a run of keys with one signature the non-causal predicate is
+// Threads 0..127 build the rows (query q0 + tid against the tile's keys),
+// threads 128..255 the columns (key k0 + tid - 128 against the queries); each
+// wave finds the run starts of the other side itself.  A row is built run by
+// run: within a run of keys with one signature the non-causal predicate is
 // constant, so one evaluation sets a whole bit range; the causal and padding
 // limits are applied last.
+template <int KW>
 __global__ __launch_bounds__(kThreads) void mask_tile_bits(
     const int32_t* __restrict__ doc_all, const uint64_t* __restrict__ qbits_all,
     const uint64_t* __restrict__ kvbits_all, int T, int words, MaskOut out) {
-  extern __shared__ __align__(16) unsigned char sig_lds[];
-  __shared__ int q_starts[kTile + 1], kv_starts[kTile + 1];
-  __shared__ int n_qr, n_kr;
   __shared__ int red[2 * kThreads / 64];
-  TileSigs qs, ks;
-  sig_views(sig_lds, words, qs, ks);
   const int nt = out.nt;
   const int b = blockIdx.y;
   int qt, kt;
   tri_tile(blockIdx.x, qt, kt);
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x;
   if (kt == 0) rank_row_col(out, b, qt, red);
   if (out.tile_class[((size_t)b * nt + qt) * nt + kt] != kPartial) return;
   const int32_t* doc = doc_all + (size_t)b * T;
+  const uint64_t* qbits = qbits_all + (size_t)b * words * T;
+  const uint64_t* kbits = kvbits_all + (size_t)b * words * T;
   const int q0 = qt * kTile, k0 = kt * kTile;
-  if (tid < kTile)
-    load_sigs(qs, doc, qbits_all + (size_t)b * words * T, words, T, q0, tid);
-  else
-    load_sigs(ks, doc, kvbits_all + (size_t)b * words * T, words, T, k0, tid - kTile);
-  __syncthreads();
-  if (wave == 0) {
-    const int n = wave_runs(qs, words, min(kTile, T - q0), q_starts);
-    if (lane == 0) n_qr = n;
-  } else if (wave == 1) {
-    const int n = wave_runs(ks, words, min(kTile, T - k0), kv_starts);
-    if (lane == 0) n_kr = n;
-  }
-  __syncthreads();
+  const bool rows = tid < kTile;
+  // this thread's token and the other side of the tile
+  const int mine = rows ? q0 + tid : k0 + tid - kTile;
+  const int obase = rows ? k0 : q0;
+  const uint64_t* mbits = rows ? qbits : kbits;
+  const uint64_t* obits = rows ? kbits : qbits;
+  const int ovalid = min(kTile, T - obase);
+  const TileSide<KW> os = wave_tile_side<KW>(doc, obits, words, T, obase, ovalid);
+  const Sig<KW> my = load_sig<KW>(doc, mbits, words, T, mine);
   uint32_t acc[4] = {0u, 0u, 0u, 0u};
-  if (tid < kTile) {
-    // row orientation: query q0 + tid against the tile's keys
-    const int r = tid, q = q0 + r;
-    if (q < T) {
-      for (int s = 0; s < n_kr; ++s) {
-        const int a = kv_starts[s], z = kv_starts[s + 1];
-        if (sigs_allowed(qs, r, ks, a, words)) set_bit_range(acc, a, z);
-      }
-      // causal: keys k0 + kk <= q; padding keys (>= T) are outside every run
-      const int lim = q - k0 + 1;  // allowed kk < lim
-      uint32_t cm[4] = {0u, 0u, 0u, 0u};
-      set_bit_range(cm, 0, min(max(lim, 0), kTile));
-#pragma unroll
-      for (int w = 0; w < 4; ++w) acc[w] &= cm[w];
-    }
-  } else {
-    // column orientation: key k0 + c against the tile's queries
-    const int c = tid - kTile, key = k0 + c;
-    if (key < T) {
-      for (int s = 0; s < n_qr; ++s) {
-        const int a = q_starts[s], z = q_starts[s + 1];
-        if (sigs_allowed(qs, a, ks, c, words)) set_bit_range(acc, a, z);
-      }
-      // causal: queries q0 + qq >= key
-      const int from = key - q0;  // allowed qq >= from
-      uint32_t cm[4] = {0u, 0u, 0u, 0u};
-      set_bit_range(cm, min(max(from, 0), kTile), kTile);
-#pragma unroll
-      for (int w = 0; w < 4; ++w) acc[w] &= cm[w];
+  // run starts of the other side, in order (a wave-uniform loop over every
+  // lane); a run's signature is that of its first token, read from the lane
+  // holding it
+  for (int h = 0; h < 2; ++h) {
+    for (uint64_t m = os.m[h]; m; m &= m - 1) {
+      const int a = 64 * h + __ffsll((long long)m) - 1;
+      const uint64_t rest = m & (m - 1);
+      const int z = rest ? 64 * h + __ffsll((long long)rest) - 1
+                         : (h == 0 && os.m[1] ? __ffsll((long long)os.m[1]) - 1 + 64 : ovalid);
+      const Sig<KW> other = readlane_sig(os.sig[h], a & 63, words);
+      if (rows ? sig_allowed(my, other, words) : sig_allowed(other, my, words))
+        set_bit_range(acc, a, z);
     }
   }
+  uint32_t cm[4] = {0u, 0u, 0u, 0u};
+  if (mine < T) {
+    if (rows) {
+      // causal: keys k0 + kk <= q; padding keys (>= T) are outside every run
+      set_bit_range(cm, 0, min(max(mine - k0 + 1, 0), kTile));
+    } else {
+      // causal: queries q0 + qq >= key
+      set_bit_range(cm, min(max(mine - q0, 0), kTile), kTile);
+    }
+  }
+  // (a token past T keeps no bit: its causal mask is empty)
+#pragma unroll
+  for (int w = 0; w < 4; ++w) acc[w] &= cm[w];
   const int slot = tri_slot(b, nt, qt) + kt;
-  uint32_t* dst = out.tile_bits + (size_t)slot * kTileBitsWords +
-                  (tid < kTile ? tid * 4 : kTile * 4 + (tid - kTile) * 4);
+  uint32_t* dst = out.tile_bits + (size_t)slot * kTileBitsWords + tid * 4;
   *reinterpret_cast<uint4*>(dst) = make_uint4(acc[0], acc[1], acc[2], acc[3]);
 }
 
@@ -389,17 +458,36 @@ hipError_t launch_mask_meta(const int32_t* doc, const uint64_t* qbits, const uin
                             int T, int words, const MaskOut& out, hipStream_t stream) {
   const int nt = out.nt;
   if (nt == 0 || out.Bm == 0) return hipSuccess;
-  const dim3 tiles((unsigned)((int64_t)nt * (nt + 1) / 2), out.Bm);
-  const int sig_bytes = sig_lds_bytes(words);
-  hipLaunchKernelGGL(mask_classify_tiles, tiles, dim3(128), sig_bytes, stream, doc, qbits, kvbits,
-                     T, words, out);
+  const int64_t n_tri = (int64_t)nt * (nt + 1) / 2;
+  const dim3 tiles((unsigned)n_tri, out.Bm);
+  const dim3 tile_quads((unsigned)((n_tri + kClassifyWaves - 1) / kClassifyWaves), out.Bm);
+  // signature registers sized for the smallest bound >= words
+  auto classify = mask_classify_tiles<8>;
+  auto bits = mask_tile_bits<8>;
+  if (words == 0) {
+    classify = mask_classify_tiles<0>;
+    bits = mask_tile_bits<0>;
+  } else if (words == 1) {
+    classify = mask_classify_tiles<1>;
+    bits = mask_tile_bits<1>;
+  } else if (words == 2) {
+    classify = mask_classify_tiles<2>;
+    bits = mask_tile_bits<2>;
+  } else if (words == 3) {
+    classify = mask_classify_tiles<3>;
+    bits = mask_tile_bits<3>;
+  } else if (words == 4) {
+    classify = mask_classify_tiles<4>;
+    bits = mask_tile_bits<4>;
+  }
+  hipLaunchKernelGGL(classify, tile_quads, dim3(kThreads), 0, stream, doc, qbits, kvbits, T,
+                     words, out);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(mask_lists, dim3(nt, out.Bm), dim3(kThreads), 0, stream, out);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(mask_tile_bits, tiles, dim3(kThreads), sig_bytes, stream, doc, qbits, kvbits,
-                     T, words, out);
+  hipLaunchKernelGGL(bits, tiles, dim3(kThreads), 0, stream, doc, qbits, kvbits, T, words, out);
   return hipGetLastError();
 }
 

@@ -47,6 +47,15 @@ def test_ragged_random(T, words, gpu_device):
     _run(rows, gpu_device, f"ragged T={T} W={words}")
 
 
+@pytest.mark.parametrize("T,words", [(300, 0), (1000, 2), (2100, 8)])
+def test_many_short_runs(T, words, gpu_device):
+    # documents of 1-2 tokens: 60-120 runs per 128-token tile side, so the
+    # run-pair loop takes many passes and run starts fall in both 64-token halves
+    rng = np.random.default_rng(T + words)
+    rows = [random_row(T, rng, words=words, uncovered=True, max_doc=3) for _ in range(2)]
+    _run(rows, gpu_device, f"short runs T={T} W={words}")
+
+
 def test_max_words_and_batch(gpu_device):
     rng = np.random.default_rng(5)
     rows = [random_row(777, rng, words=8, uncovered=True) for _ in range(3)]
