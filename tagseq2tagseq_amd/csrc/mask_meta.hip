@@ -21,18 +21,20 @@
 // rectangle.  Packed documents give 1-3 runs per 128 tokens, so a tile costs a
 // handful of evaluations instead of 16384.
 //
-// Launches: (1) classify every tile, (2) row and column lists with the
-// bitmap slot tables, (3) partial-tile bitmaps; in the third each row's
-// column-0 work-group also ranks its row and column for the launch orders,
-// so no launch waits on a single work-group.  The bitmap of tile (b, qt, kt) lives in slot
-// b * nt (nt + 1) / 2 + qt (qt + 1) / 2 + kt (a fixed position in the lower
-// triangle), so no work-group has to count the partial tiles before its own.
-// The runs are found in registers: each lane loads the signatures (doc id,
-// grant words) of its tokens and of the tokens just before them, a ballot of
-// "differs from the previous token" marks the run starts of 128 tokens as a
-// 128-bit mask, and the signature of a run is read at its first token (a
-// cached load); no work-group stages signatures in LDS or waits at a barrier
-// for them.
+// Launches: (1) one wave per tile of the lower triangle: its class and, for a
+// partial tile, both orientations of its bitmap; (2) row and column lists with
+// the bitmap slot tables; (3) launch orders, each row's work-group ranking
+// its row and its column (no launch waits on a single work-group).  The
+// bitmap of tile (b, qt, kt) lives in slot b * nt (nt + 1) / 2 + qt (qt + 1) / 2
+// + kt (a fixed position in the lower triangle), so no wave has to count the
+// partial tiles before its own.
+// The runs are found in registers: lane l of a wave holds the signatures
+// (doc id, grant words) of tokens l and 64 + l of a tile side, a whole-wave
+// lane shift compares each token with the one before it, and a ballot marks
+// the run starts of the 128 tokens as a 128-bit mask; a run's signature is
+// that of its first token, read from the lane holding it.  The grant-word
+// count is a template parameter, so a signature is exactly the registers it
+// needs and no loop over words is decided at run time.
 #include "attn_kernels.h"
 
 namespace t2t {
@@ -48,43 +50,64 @@ __device__ __forceinline__ void tri_tile(int L, int& qt, int& kt) {
   kt = L - (int)((int64_t)r * (r + 1) / 2);
 }
 
-// A token's signature: document id and grant words (zeros past T).  KW is
-// the compile-time bound on the words (registers are held for KW of them);
-// the `words` arguments below give how many are real (words <= KW).
-template <int KW>
+// First bitmap slot of mask row b's tile row qt (slot of tile (qt, kt) =
+// this + kt).
+// (t2t_mask_meta keeps every slot index below 2^31.)
+__device__ __forceinline__ int tri_slot(int b, int nt, int qt) {
+  return (int)((int64_t)b * ((int64_t)nt * (nt + 1) / 2) + (int64_t)qt * (qt + 1) / 2);
+}
+
+// Set bits [lo, hi) of a 128-bit mask held as four 32-bit words.
+__device__ __forceinline__ void set_bit_range(uint32_t acc[4], int lo, int hi) {
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const int a = max(lo - 32 * w, 0), z = min(hi - 32 * w, 32);
+    if (a < z) {
+      const uint32_t upto = z == 32 ? ~0u : ((1u << z) - 1u);
+      acc[w] |= upto & ~((1u << a) - 1u);
+    }
+  }
+}
+
+// A token's signature: document id and W grant words (zeros past T).
+template <int W>
 struct Sig {
   int32_t doc;
-  uint64_t w[KW > 0 ? KW : 1];
+  uint64_t w[W > 0 ? W : 1];
 };
 
-template <int KW>
-__device__ __forceinline__ Sig<KW> load_sig(const int32_t* doc, const uint64_t* bits, int words,
-                                            int T, int t) {
-  Sig<KW> g;
+template <int W>
+__device__ __forceinline__ Sig<W> load_sig(const int32_t* doc, const uint64_t* bits, int T,
+                                           int t) {
+  // loads from a clamped index (T >= 1), so that none sits in a branch
+  const int tc = min(t, T - 1);
   const bool in = t < T;
-  g.doc = in ? doc[t] : 0;
+  Sig<W> g;
+  const int32_t d = doc[tc];
+  g.doc = in ? d : 0;
 #pragma unroll
-  for (int w = 0; w < KW; ++w) g.w[w] = (in && w < words) ? bits[(size_t)w * T + t] : 0ull;
+  for (int w = 0; w < W; ++w) {
+    const uint64_t v = bits[(size_t)w * T + tc];
+    g.w[w] = in ? v : 0ull;
+  }
   return g;
 }
 
-template <int KW>
-__device__ __forceinline__ bool sig_eq(const Sig<KW>& a, const Sig<KW>& b, int words) {
+template <int W>
+__device__ __forceinline__ bool sig_eq(const Sig<W>& a, const Sig<W>& b) {
   bool eq = a.doc == b.doc;
 #pragma unroll
-  for (int w = 0; w < KW; ++w)
-    if (w < words) eq = eq && a.w[w] == b.w[w];
+  for (int w = 0; w < W; ++w) eq = eq && a.w[w] == b.w[w];
   return eq;
 }
 
 // The non-causal part of the predicate for a query-side signature q and a
 // key-side signature k: same document, or a shared grant bit.
-template <int KW>
-__device__ __forceinline__ bool sig_allowed(const Sig<KW>& q, const Sig<KW>& k, int words) {
+template <int W>
+__device__ __forceinline__ bool sig_allowed(const Sig<W>& q, const Sig<W>& k) {
   bool ok = q.doc == k.doc;
 #pragma unroll
-  for (int w = 0; w < KW; ++w)
-    if (w < words) ok = ok || (q.w[w] & k.w[w]) != 0ull;
+  for (int w = 0; w < W; ++w) ok = ok || (q.w[w] & k.w[w]) != 0ull;
   return ok;
 }
 
@@ -95,37 +118,37 @@ __device__ __forceinline__ int lanes_below(uint64_t mask) {
                                    __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0));
 }
 
-// Lane src's signature, fetched by every lane (src may differ per lane).
-template <int KW>
-__device__ __forceinline__ Sig<KW> shfl_sig(const Sig<KW>& g, int src, int words) {
-  Sig<KW> r;
-  r.doc = __shfl(g.doc, src, 64);
-#pragma unroll
-  for (int w = 0; w < KW; ++w) {
-    r.w[w] = 0ull;
-    if (w < words) {
-      const uint32_t lo = (uint32_t)__shfl((int)(uint32_t)g.w[w], src, 64);
-      const uint32_t hi = (uint32_t)__shfl((int)(uint32_t)(g.w[w] >> 32), src, 64);
-      r.w[w] = ((uint64_t)hi << 32) | lo;
-    }
-  }
-  return r;
+__device__ __forceinline__ uint64_t join64(uint32_t lo, uint32_t hi) {
+  return ((uint64_t)hi << 32) | lo;
 }
 
 // Lane src's signature (src the same for every lane).
-template <int KW>
-__device__ __forceinline__ Sig<KW> readlane_sig(const Sig<KW>& g, int src, int words) {
-  Sig<KW> r;
+template <int W>
+__device__ __forceinline__ Sig<W> readlane_sig(const Sig<W>& g, int src) {
+  Sig<W> r;
   r.doc = __builtin_amdgcn_readlane(g.doc, src);
 #pragma unroll
-  for (int w = 0; w < KW; ++w) {
-    r.w[w] = 0ull;
-    if (w < words) {
-      const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)g.w[w], src);
-      const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(g.w[w] >> 32), src);
-      r.w[w] = ((uint64_t)hi << 32) | lo;
-    }
-  }
+  for (int w = 0; w < W; ++w)
+    r.w[w] = join64((uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)g.w[w], src),
+                    (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(g.w[w] >> 32), src));
+  return r;
+}
+
+// Every lane's predecessor within the wave (lane l gets lane l - 1's
+// signature; lane 0 gets `first`): a whole-wave right shift by one lane (DPP).
+__device__ __forceinline__ int shift_up(int first, int v) {
+  return __builtin_amdgcn_update_dpp(first, v, 0x138, 0xf, 0xf, false);
+}
+
+template <int W>
+__device__ __forceinline__ Sig<W> shift_up_sig(const Sig<W>& g, const Sig<W>& first) {
+  Sig<W> r;
+  r.doc = shift_up(first.doc, g.doc);
+#pragma unroll
+  for (int w = 0; w < W; ++w)
+    r.w[w] = join64((uint32_t)shift_up((int)(uint32_t)first.w[w], (int)(uint32_t)g.w[w]),
+                    (uint32_t)shift_up((int)(uint32_t)(first.w[w] >> 32),
+                                       (int)(uint32_t)(g.w[w] >> 32)));
   return r;
 }
 
@@ -134,83 +157,46 @@ __device__ __forceinline__ Sig<KW> readlane_sig(const Sig<KW>& g, int src, int w
 // base + 64 + l (sig[1]).  Bit i of the 128-bit run mask (m[0] bits 0-63,
 // m[1] bits 64-127) is set iff token base + i starts a run of identical
 // signatures.
-template <int KW>
+template <int W>
 struct TileSide {
-  Sig<KW> sig[2];
+  Sig<W> sig[2];
   uint64_t m[2];
 };
 
-template <int KW>
-__device__ __forceinline__ TileSide<KW> wave_tile_side(const int32_t* doc, const uint64_t* bits,
-                                                       int words, int T, int base, int nvalid) {
+// Marks the run starts of a side whose signatures the wave already holds.
+template <int W>
+__device__ __forceinline__ TileSide<W> mark_runs(const Sig<W>& s0, const Sig<W>& s1, int nvalid) {
   const int lane = lane_id();
-  TileSide<KW> s;
-  s.sig[0] = load_sig<KW>(doc, bits, words, T, base + lane);
-  s.sig[1] = load_sig<KW>(doc, bits, words, T, base + 64 + lane);
+  TileSide<W> s;
+  s.sig[0] = s0;
+  s.sig[1] = s1;
   // predecessor of each token: lane - 1 of the same half; lane 0 of the
-  // second half takes lane 63 of the first
-  const int up = (lane + 63) & 63;
-  const Sig<KW> p0 = shfl_sig(s.sig[0], up, words);
-  const Sig<KW> t1 = shfl_sig(s.sig[1], up, words);
-  const Sig<KW> p1 = lane == 0 ? p0 : t1;
-  const bool f0 = lane < nvalid && (lane == 0 || !sig_eq(s.sig[0], p0, words));
-  const bool f1 = 64 + lane < nvalid && !sig_eq(s.sig[1], p1, words);
+  // second half takes lane 63 of the first (lane 0 of the first half starts
+  // a run whatever it is compared with)
+  const Sig<W> last0 = readlane_sig(s0, 63);
+  const Sig<W> p0 = shift_up_sig(s0, last0);
+  const Sig<W> p1 = shift_up_sig(s1, last0);
+  const bool f0 = lane < nvalid && (lane == 0 || !sig_eq(s0, p0));
+  const bool f1 = 64 + lane < nvalid && !sig_eq(s1, p1);
   s.m[0] = __ballot(f0);
   s.m[1] = __ballot(f1);
   return s;
 }
 
-// The signature of token i of the side, for every lane's own i.
-template <int KW>
-__device__ __forceinline__ Sig<KW> side_sig(const TileSide<KW>& s, int i, int words) {
-  const Sig<KW> lo = shfl_sig(s.sig[0], i & 63, words);
-  const Sig<KW> hi = shfl_sig(s.sig[1], i & 63, words);
-  return i < 64 ? lo : hi;
-}
-
-// The run starts as a mask pair, for the helpers below.
-struct RunMask {
-  uint64_t m[2];
-};
-
-template <int KW>
-__device__ __forceinline__ RunMask run_mask(const TileSide<KW>& s) {
-  return RunMask{{s.m[0], s.m[1]}};
-}
-
-__device__ __forceinline__ int run_count(const RunMask& r) {
-  return __popcll(r.m[0]) + __popcll(r.m[1]);
-}
-
-// Position of the n-th (0-based) run start, or `none` when there are n or
-// fewer starts (the end of the last run).
-__device__ __forceinline__ int nth_start(const RunMask& r, int n, int none) {
-  const int c0 = __popcll(r.m[0]);
-  uint64_t m = r.m[0];
-  int pos = 0;
-  if (n >= c0) {
-    m = r.m[1];
-    pos = 64;
-    n -= c0;
-  }
-  if (n >= __popcll(m)) return none;
+// Calls f(a, z, sig) for every run [a, z) of the side in order (a
+// wave-uniform loop; sig = the run's signature) while go() holds.
+template <int W, class F, class G>
+__device__ __forceinline__ void for_each_run(const TileSide<W>& s, int nvalid, G go, F f) {
 #pragma unroll
-  for (int width = 32; width >= 1; width >>= 1) {
-    const int c = __popcll(m & ((1ull << width) - 1ull));
-    if (n >= c) {
-      n -= c;
-      m >>= width;
-      pos += width;
+  for (int h = 0; h < 2; ++h) {
+    for (uint64_t m = s.m[h]; m && go(); m &= m - 1) {
+      const int a = 64 * h + __ffsll((long long)m) - 1;
+      const uint64_t rest = m & (m - 1);
+      const int z = rest ? 64 * h + __ffsll((long long)rest) - 1
+                         : (h == 0 && s.m[1] ? 64 + __ffsll((long long)s.m[1]) - 1 : nvalid);
+      f(a, z, readlane_sig(s.sig[h], a & 63));
     }
   }
-  return pos;
-}
-
-// First bitmap slot of mask row b's tile row qt (slot of tile (qt, kt) =
-// this + kt).
-// (t2t_mask_meta keeps every slot index below 2^31.)
-__device__ __forceinline__ int tri_slot(int b, int nt, int qt) {
-  return (int)((int64_t)b * ((int64_t)nt * (nt + 1) / 2) + (int64_t)qt * (qt + 1) / 2);
 }
 
 // Compact one 0/1 row of `n` byte flags (flag = (cls == want)) into the
@@ -248,57 +234,104 @@ __device__ void wave_ordered(const int8_t* cls, int stride, int n, int8_t want,
 
 }  // namespace
 
-// (1) grid (ceil(nt (nt + 1) / 2 / 4), Bm); block 256: each wave decides one
+// (1) grid (ceil(nt (nt + 1) / 2 / 4), Bm); block 256: each wave takes one
 // tile of the lower triangle (kt <= qt; linear index 4 x + wave, row-major)
 // and writes its mirror above the diagonal as skip (every pair there has
-// kv > q).  The wave finds the query and key run starts and evaluates the
-// run pairs, 64 at a time, stopping once the tile is known to be partial.
-constexpr int kClassifyWaves = kThreads / 64;
+// kv > q).  Class: each query run against every key token (lanes over key
+// tokens, a loop over query runs), stopping once the tile is known to be
+// partial.
+// Bitmap of a partial tile: lane l builds rows l and 64 + l (those queries
+// against the key runs) and columns l and 64 + l (those keys against the
+// query runs); within a run the non-causal predicate is constant, so one
+// evaluation sets a whole bit range; the causal and padding limits come last.
+constexpr int kTileWaves = kThreads / 64;
 
-template <int KW>
-__global__ __launch_bounds__(kThreads) void mask_classify_tiles(
-    const int32_t* __restrict__ doc_all, const uint64_t* __restrict__ qbits_all,
-    const uint64_t* __restrict__ kvbits_all, int T, int words, MaskOut out) {
+template <int W>
+__global__ __launch_bounds__(kThreads) void mask_tiles(const int32_t* __restrict__ doc_all,
+                                                       const uint64_t* __restrict__ qbits_all,
+                                                       const uint64_t* __restrict__ kvbits_all,
+                                                       int T, MaskOut out) {
   const int nt = out.nt;
   const int b = blockIdx.y;
-  const int64_t L = (int64_t)blockIdx.x * kClassifyWaves + (threadIdx.x >> 6);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t L = (int64_t)blockIdx.x * kTileWaves + wave;
   if (L >= (int64_t)nt * (nt + 1) / 2) return;
   int qt, kt;
   tri_tile((int)L, qt, kt);
   const int lane = lane_id();
   if (lane == 0 && kt < qt) out.tile_class[((size_t)b * nt + kt) * nt + qt] = kSkip;
   const int32_t* doc = doc_all + (size_t)b * T;
-  const uint64_t* qbits = qbits_all + (size_t)b * words * T;
-  const uint64_t* kbits = kvbits_all + (size_t)b * words * T;
   const int q0 = qt * kTile, k0 = kt * kTile;
   const int qvalid = min(kTile, T - q0), kvalid = min(kTile, T - k0);
-  const TileSide<KW> qs = wave_tile_side<KW>(doc, qbits, words, T, q0, qvalid);
-  const TileSide<KW> ks = wave_tile_side<KW>(doc, kbits, words, T, k0, kvalid);
-  const RunMask qr = run_mask(qs), kr = run_mask(ks);
-  const int nqr = run_count(qr), nkr = run_count(kr);
+  // query tokens q0 + lane and q0 + 64 + lane, key tokens k0 + lane and
+  // k0 + 64 + lane
+  const uint64_t* qbits = qbits_all + (size_t)b * W * T;
+  const uint64_t* kbits = kvbits_all + (size_t)b * W * T;
+  const Sig<W> qsig[2] = {load_sig<W>(doc, qbits, T, q0 + lane),
+                          load_sig<W>(doc, qbits, T, q0 + 64 + lane)};
+  const Sig<W> ksig[2] = {load_sig<W>(doc, kbits, T, k0 + lane),
+                          load_sig<W>(doc, kbits, T, k0 + 64 + lane)};
+  const TileSide<W> qs = mark_runs(qsig[0], qsig[1], qvalid);
   // Padding rows/columns are False pairs: such a tile can never be full.
   bool any_true = false;
   bool any_false = (qvalid < kTile) || (kvalid < kTile);
-  const int npairs = nqr * nkr;
-  for (int p0 = 0; p0 < npairs; p0 += 64) {
-    const int p = p0 + lane;
-    const int r = min(p, npairs - 1) / nkr, c = min(p, npairs - 1) - r * nkr;
-    const int qa = nth_start(qr, r, 0), qb = nth_start(qr, r + 1, qvalid);
-    const int ka = nth_start(kr, c, 0), kb = nth_start(kr, c + 1, kvalid);
-    // every lane takes part in the shuffles (lanes past the last pair
-    // repeat it)
-    const bool v = sig_allowed(side_sig(qs, qa, words), side_sig(ks, ka, words), words);
-    const bool exists_ge = (q0 + qb - 1) >= (k0 + ka);  // some pair with q >= kv
-    const bool exists_lt = (q0 + qa) < (k0 + kb - 1);   // some pair with q < kv
-    const bool t = v && exists_ge;
-    const bool f = !v || exists_lt;
+  auto open = [&]() { return !(any_true && any_false); };
+  // each query run against every key token: within the run the non-causal
+  // predicate is constant, and the run's first and last query bound the
+  // causal part
+  for_each_run(qs, qvalid, open, [&](int qa, int qb, const Sig<W>& rsig) {
+    bool t = false, f = false;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int kk = lane + 64 * i;
+      const bool v = sig_allowed(rsig, ksig[i]);
+      const bool exists_ge = q0 + qb - 1 >= k0 + kk;  // some pair with q >= kv
+      const bool exists_lt = q0 + qa < k0 + kk;       // some pair with q < kv
+      t = t || (kk < kvalid && v && exists_ge);
+      f = f || (kk < kvalid && (!v || exists_lt));
+    }
     any_true = any_true || (__ballot(t) != 0);
     any_false = any_false || (__ballot(f) != 0);
-    if (any_true && any_false) break;
+  });
+  const int8_t cls = any_true ? (any_false ? kPartial : kFull) : kSkip;
+  if (lane == 0) out.tile_class[((size_t)b * nt + qt) * nt + kt] = cls;
+  if (cls != kPartial) return;
+
+  const TileSide<W> ks = mark_runs(ksig[0], ksig[1], kvalid);
+  auto always = []() { return true; };
+  uint32_t rows[2][4] = {}, cols[2][4] = {};
+  for_each_run(ks, kvalid, always, [&](int a, int z, const Sig<W>& rsig) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      if (sig_allowed(qsig[i], rsig)) set_bit_range(rows[i], a, z);
+  });
+  for_each_run(qs, qvalid, always, [&](int a, int z, const Sig<W>& rsig) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      if (sig_allowed(rsig, ksig[i])) set_bit_range(cols[i], a, z);
+  });
+  uint32_t* dst = out.tile_bits + (size_t)(tri_slot(b, nt, qt) + kt) * kTileBitsWords;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int t = lane + 64 * i;
+    // causal: query q0 + t sees keys k0 + kk <= q0 + t; key k0 + t is seen by
+    // queries q0 + qq >= k0 + t; tokens past T keep no bit (padding keys and
+    // queries lie outside every run)
+    uint32_t rm[4] = {}, cm[4] = {};
+    if (kt < qt) {
+      // below the diagonal every key precedes every query
+      const uint32_t all = q0 + t < T ? ~0u : 0u;
+      rm[0] = rm[1] = rm[2] = rm[3] = all;
+      cm[0] = cm[1] = cm[2] = cm[3] = ~0u;
+    } else {
+      if (q0 + t < T) set_bit_range(rm, 0, min(max(q0 + t - k0 + 1, 0), kTile));
+      if (k0 + t < T) set_bit_range(cm, min(max(k0 + t - q0, 0), kTile), kTile);
+    }
+    *reinterpret_cast<uint4*>(dst + t * 4) =
+        make_uint4(rows[i][0] & rm[0], rows[i][1] & rm[1], rows[i][2] & rm[2], rows[i][3] & rm[3]);
+    *reinterpret_cast<uint4*>(dst + (kTile + t) * 4) =
+        make_uint4(cols[i][0] & cm[0], cols[i][1] & cm[1], cols[i][2] & cm[2], cols[i][3] & cm[3]);
   }
-  if (lane == 0)
-    out.tile_class[((size_t)b * nt + qt) * nt + kt] =
-        any_true ? (any_false ? kPartial : kFull) : kSkip;
 }
 
 // (2) grid (nt, Bm); block 256.  Wave 0/1: partial / full list of row x
@@ -371,123 +404,32 @@ __device__ void rank_row_col(const MaskOut& out, int b, int i, int* red) {
 
 }  // namespace
 
-namespace {
-
-// Set bits [lo, hi) of a 128-bit mask held as four 32-bit words.
-__device__ __forceinline__ void set_bit_range(uint32_t acc[4], int lo, int hi) {
-#pragma unroll
-  for (int w = 0; w < 4; ++w) {
-    const int a = max(lo - 32 * w, 0), z = min(hi - 32 * w, 32);
-    if (a < z) {
-      const uint32_t upto = z == 32 ? ~0u : ((1u << z) - 1u);
-      acc[w] |= upto & ~((1u << a) - 1u);
-    }
-  }
-}
-
-}  // namespace
-
-// (3) grid (nt (nt + 1) / 2, Bm); block 256.  For a partial tile of the lower
-// triangle: both bitmap orientations, into slot tri_slot(b, nt, qt) + kt.
-// Work-group (qt, 0) also ranks row qt and column qt for the launch orders.
-// Threads 0..127 build the rows (query q0 + tid against the tile's keys),
-// threads 128..255 the columns (key k0 + tid - 128 against the queries); each
-// wave finds the run starts of the other side itself.  A row is built run by
-// run: within a run of keys with one signature the non-causal predicate is
-// constant, so one evaluation sets a whole bit range; the causal and padding
-// limits are applied last.
-template <int KW>
-__global__ __launch_bounds__(kThreads) void mask_tile_bits(
-    const int32_t* __restrict__ doc_all, const uint64_t* __restrict__ qbits_all,
-    const uint64_t* __restrict__ kvbits_all, int T, int words, MaskOut out) {
+// (3) grid (nt, Bm); block 256: the launch-order ranks of row x and column x.
+__global__ __launch_bounds__(kThreads) void mask_rank(MaskOut out) {
   __shared__ int red[2 * kThreads / 64];
-  const int nt = out.nt;
-  const int b = blockIdx.y;
-  int qt, kt;
-  tri_tile(blockIdx.x, qt, kt);
-  const int tid = threadIdx.x;
-  if (kt == 0) rank_row_col(out, b, qt, red);
-  if (out.tile_class[((size_t)b * nt + qt) * nt + kt] != kPartial) return;
-  const int32_t* doc = doc_all + (size_t)b * T;
-  const uint64_t* qbits = qbits_all + (size_t)b * words * T;
-  const uint64_t* kbits = kvbits_all + (size_t)b * words * T;
-  const int q0 = qt * kTile, k0 = kt * kTile;
-  const bool rows = tid < kTile;
-  // this thread's token and the other side of the tile
-  const int mine = rows ? q0 + tid : k0 + tid - kTile;
-  const int obase = rows ? k0 : q0;
-  const uint64_t* mbits = rows ? qbits : kbits;
-  const uint64_t* obits = rows ? kbits : qbits;
-  const int ovalid = min(kTile, T - obase);
-  const TileSide<KW> os = wave_tile_side<KW>(doc, obits, words, T, obase, ovalid);
-  const Sig<KW> my = load_sig<KW>(doc, mbits, words, T, mine);
-  uint32_t acc[4] = {0u, 0u, 0u, 0u};
-  // run starts of the other side, in order (a wave-uniform loop over every
-  // lane); a run's signature is that of its first token, read from the lane
-  // holding it
-  for (int h = 0; h < 2; ++h) {
-    for (uint64_t m = os.m[h]; m; m &= m - 1) {
-      const int a = 64 * h + __ffsll((long long)m) - 1;
-      const uint64_t rest = m & (m - 1);
-      const int z = rest ? 64 * h + __ffsll((long long)rest) - 1
-                         : (h == 0 && os.m[1] ? __ffsll((long long)os.m[1]) - 1 + 64 : ovalid);
-      const Sig<KW> other = readlane_sig(os.sig[h], a & 63, words);
-      if (rows ? sig_allowed(my, other, words) : sig_allowed(other, my, words))
-        set_bit_range(acc, a, z);
-    }
-  }
-  uint32_t cm[4] = {0u, 0u, 0u, 0u};
-  if (mine < T) {
-    if (rows) {
-      // causal: keys k0 + kk <= q; padding keys (>= T) are outside every run
-      set_bit_range(cm, 0, min(max(mine - k0 + 1, 0), kTile));
-    } else {
-      // causal: queries q0 + qq >= key
-      set_bit_range(cm, min(max(mine - q0, 0), kTile), kTile);
-    }
-  }
-  // (a token past T keeps no bit: its causal mask is empty)
-#pragma unroll
-  for (int w = 0; w < 4; ++w) acc[w] &= cm[w];
-  const int slot = tri_slot(b, nt, qt) + kt;
-  uint32_t* dst = out.tile_bits + (size_t)slot * kTileBitsWords + tid * 4;
-  *reinterpret_cast<uint4*>(dst) = make_uint4(acc[0], acc[1], acc[2], acc[3]);
+  rank_row_col(out, blockIdx.y, blockIdx.x, red);
 }
 
 hipError_t launch_mask_meta(const int32_t* doc, const uint64_t* qbits, const uint64_t* kvbits,
                             int T, int words, const MaskOut& out, hipStream_t stream) {
   const int nt = out.nt;
   if (nt == 0 || out.Bm == 0) return hipSuccess;
+  if (words < 0 || words > kMaxWords) return hipErrorInvalidValue;
   const int64_t n_tri = (int64_t)nt * (nt + 1) / 2;
-  const dim3 tiles((unsigned)n_tri, out.Bm);
-  const dim3 tile_quads((unsigned)((n_tri + kClassifyWaves - 1) / kClassifyWaves), out.Bm);
-  // signature registers sized for the smallest bound >= words
-  auto classify = mask_classify_tiles<8>;
-  auto bits = mask_tile_bits<8>;
-  if (words == 0) {
-    classify = mask_classify_tiles<0>;
-    bits = mask_tile_bits<0>;
-  } else if (words == 1) {
-    classify = mask_classify_tiles<1>;
-    bits = mask_tile_bits<1>;
-  } else if (words == 2) {
-    classify = mask_classify_tiles<2>;
-    bits = mask_tile_bits<2>;
-  } else if (words == 3) {
-    classify = mask_classify_tiles<3>;
-    bits = mask_tile_bits<3>;
-  } else if (words == 4) {
-    classify = mask_classify_tiles<4>;
-    bits = mask_tile_bits<4>;
-  }
-  hipLaunchKernelGGL(classify, tile_quads, dim3(kThreads), 0, stream, doc, qbits, kvbits, T,
-                     words, out);
+  const dim3 tiles((unsigned)((n_tri + kTileWaves - 1) / kTileWaves), out.Bm);
+  using TilesFn = void (*)(const int32_t*, const uint64_t*, const uint64_t*, int, MaskOut);
+  static constexpr TilesFn kTilesByWords[kMaxWords + 1] = {
+      mask_tiles<0>, mask_tiles<1>, mask_tiles<2>, mask_tiles<3>, mask_tiles<4>,
+      mask_tiles<5>, mask_tiles<6>, mask_tiles<7>, mask_tiles<8>};
+  static_assert(kMaxWords == 8, "one instantiation per grant-word count");
+  hipLaunchKernelGGL(kTilesByWords[words], tiles, dim3(kThreads), 0, stream, doc, qbits, kvbits,
+                     T, out);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(mask_lists, dim3(nt, out.Bm), dim3(kThreads), 0, stream, out);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(bits, tiles, dim3(kThreads), 0, stream, doc, qbits, kvbits, T, words, out);
+  hipLaunchKernelGGL(mask_rank, dim3(nt, out.Bm), dim3(kThreads), 0, stream, out);
   return hipGetLastError();
 }
 
