@@ -392,6 +392,30 @@ int t2t_first_input_diff(const int64_t *tokens_a, const int64_t *tokens_b, const
                          int32_t *out, void *stream);
 
 /*
+ * Cross-entropy rows of a linear head: loss and logit gradient in one pass.
+ * Replaces, per chunk of rows, torch's F.cross_entropy(logits.float(),
+ * targets, ignore_index, reduction="sum") and its backward inside the
+ * reference's FusedLinearCELoss (tunalab; constructed at
+ * model/modules/training_module.py:127-133, called at :209), which produces
+ * the gradient during the forward so that dX and dW follow without
+ * recomputing the logits.
+ *   logits   bf16 [rows][ld] (device, 16-byte aligned); columns 0 .. V-1
+ *            are the logits, columns V .. ld-1 are ignored.  ld % 8 == 0,
+ *            1 <= V <= ld.
+ *   grad     bf16 [rows][ld] out (may be `logits` itself): (softmax - onehot)
+ *            * (*scale) in columns < V, 0 in the rest.
+ *   target   int64[rows]; a row whose target equals ignore_index has loss 0
+ *            and a zero gradient; any other target outside [0, V) gives a NaN
+ *            loss (and a zero gradient).
+ *   scale    float[1] (device): the gradient's factor (e.g. 1 / number of
+ *            counted rows for a mean).
+ *   row_loss float[rows] out: logsumexp(row) - row[target], computed in fp32.
+ */
+int t2t_ce_rows(const void *logits, void *grad, int64_t rows, int32_t V, int64_t ld,
+                const int64_t *target, int64_t ignore_index, const float *scale,
+                float *row_loss, void *stream);
+
+/*
  * Engine-clock probe.  No counterpart in the reference: measurement support
  * for re-deriving the MFMA peak from the clock a box actually runs at.
  * Enqueues one kernel in which every SIMD runs two waves of back-to-back

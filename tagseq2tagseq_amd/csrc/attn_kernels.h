@@ -116,6 +116,11 @@ hipError_t launch_attn_decode(const TensorView& q, const TensorView& k, const Te
                               int B, int Hq, int Hkv, int Tq, int Tkv, int D, float scale,
                               float* workspace, hipStream_t stream);
 
+// Cross-entropy rows: loss and (softmax - onehot) * scale per bf16 row.
+hipError_t launch_ce_rows(const uint16_t* logits, uint16_t* grad, int64_t rows, int V, int64_t ld,
+                          const int64_t* target, int64_t ignore_index, const float* scale,
+                          float* row_loss, hipStream_t stream);
+
 // RMS normalisation of token rows (bf16 rows, bf16 or fp32 weight).
 int rmsnorm_bwd_groups(int N, int C);
 hipError_t launch_rmsnorm_fwd(const __bf16* x, int64_t xs, const void* w, bool w_f32, __bf16* y,

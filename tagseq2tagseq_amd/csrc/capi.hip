@@ -504,6 +504,24 @@ int t2t_rms_norm(const void* x, int64_t x_stride, const void* weight, int32_t we
                     "t2t_rms_norm launch");
 }
 
+int t2t_ce_rows(const void* logits, void* grad, int64_t rows, int32_t V, int64_t ld,
+                const int64_t* target, int64_t ignore_index, const float* scale, float* row_loss,
+                void* stream) {
+  if (rows < 0 || rows > 0x7fffffffLL) return fail(T2T_EINVAL, "rows=%lld", (long long)rows);
+  if (V < 1 || ld < V || ld % 8 != 0)
+    return fail(T2T_EINVAL, "V=%d ld=%lld: need 1 <= V <= ld and ld %% 8 == 0", V, (long long)ld);
+  if (rows == 0) return T2T_OK;
+  if (!logits || !grad || !target || !scale || !row_loss)
+    return fail(T2T_EINVAL, "logits / grad / target / scale / row_loss is NULL");
+  if ((reinterpret_cast<uintptr_t>(logits) | reinterpret_cast<uintptr_t>(grad)) & 15)
+    return fail(T2T_EINVAL, "logits and grad must be 16-byte aligned");
+  return hip_status(t2t::launch_ce_rows(static_cast<const uint16_t*>(logits),
+                                        static_cast<uint16_t*>(grad), rows, V, ld, target,
+                                        ignore_index, scale, row_loss,
+                                        static_cast<hipStream_t>(stream)),
+                    "t2t_ce_rows launch");
+}
+
 int64_t t2t_rms_norm_backward_workspace(int32_t N, int32_t C) {
   if (N <= 0 || C <= 0) return 0;
   return (int64_t)t2t::rmsnorm_bwd_groups(N, C) * C * 4;

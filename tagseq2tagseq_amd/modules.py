@@ -30,6 +30,7 @@ import torch.utils.checkpoint
 
 from . import norm
 from .attention import FlexSelfAttention
+from .head_loss import HeadCEFn, fused_head_applies
 
 
 class RMSNorm(nn.Module):
@@ -133,23 +134,31 @@ class TS2TSBackbone(nn.Module):
 
 
 class LinearCELoss(nn.Module):
-    """Linear head + mean cross-entropy, evaluated in row chunks so the full
-    [T, V] logits never exist at once (the role of tunalab's
-    FusedLinearCELoss).  ``weight`` ties the head to the embedding."""
+    """Linear head + mean cross-entropy (the role of tunalab's FusedLinearCELoss,
+    model/modules/training_module.py:127-133, 209).  bf16 rows on the GPU run
+    the fused path of ``head_loss`` (the logit gradient produced in the
+    forward by the ``t2t_ce_rows`` kernel, no recomputation, no fp32 logits;
+    ``gpu_chunk`` rows per chunk, None = as many as 2 GiB of bf16 logits
+    hold); other inputs are evaluated in row chunks of ``chunk`` with
+    recomputation, so the full [T, V] logits never exist at once.  ``weight``
+    ties the head to the embedding."""
 
     def __init__(self, D: int, V: int, dtype: torch.dtype = torch.bfloat16,
                  ignore_index: int = -100, weight: Optional[nn.Parameter] = None,
-                 chunk: int = 4096):
+                 chunk: int = 4096, gpu_chunk: Optional[int] = None):
         super().__init__()
         self.weight = weight if weight is not None else nn.Parameter(torch.empty(V, D))
         if weight is None:
             nn.init.normal_(self.weight, std=D ** -0.5)
         self.ignore_index = ignore_index
         self.chunk = chunk
+        self.gpu_chunk = gpu_chunk
 
     def forward(self, x: torch.Tensor, targets: torch.Tensor) -> torch.Tensor:
         x = x.reshape(-1, x.shape[-1])
         t = targets.reshape(-1)
+        if fused_head_applies(x, self.weight):
+            return HeadCEFn.apply(x, self.weight, t, int(self.ignore_index), self.gpu_chunk)
         n = (t != self.ignore_index).sum().clamp(min=1)
         total = x.new_zeros((), dtype=torch.float32)
         for r0 in range(0, x.shape[0], self.chunk):

@@ -315,3 +315,17 @@ def test_first_input_diff_argument_checks():
     assert lib.t2t_first_input_diff(*args(out=None)) == -1 and "out" in _err()
     assert lib.t2t_first_input_diff(*args(q=None)) == -1 and "grant-word" in _err()
     assert lib.t2t_first_input_diff(*args(sa=8)) == -1 and "stride" in _err()
+
+
+def test_ce_rows_argument_checks():
+    lib = _lib.lib()
+    P = ctypes.c_void_p(0x1000)
+    args = lambda rows=4, V=10, ld=16, lg=P, sc=P: (  # noqa: E731
+        lg, lg, rows, V, ld, P, -100, sc, P, None)
+    assert lib.t2t_ce_rows(*args(ld=12)) == -1 and "ld" in _err()
+    assert lib.t2t_ce_rows(*args(V=0)) == -1
+    assert lib.t2t_ce_rows(*args(V=17)) == -1
+    assert lib.t2t_ce_rows(*args(rows=-1)) == -1
+    assert lib.t2t_ce_rows(*args(sc=None)) == -1 and "NULL" in _err()
+    assert lib.t2t_ce_rows(*args(lg=ctypes.c_void_p(0x1002))) == -1 and "aligned" in _err()
+    assert lib.t2t_ce_rows(*args(rows=0)) == 0
