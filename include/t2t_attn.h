@@ -392,6 +392,27 @@ int t2t_first_input_diff(const int64_t *tokens_a, const int64_t *tokens_b, const
                          int32_t *out, void *stream);
 
 /*
+ * SwiGLU of the MLP: h = silu(g) * u, computed in fp32 and rounded once, from
+ * the gate / up product's rows [g | u] (g = the first H columns, u = the next
+ * H).  Replaces the activation and product inside tunalab's GLU
+ * (model/modules/layer.py:23-28; GLU(..., activation="silu")), i.e. torch's
+ * chunk + silu + multiply.
+ *   gu  bf16 [N][2H] with row stride gu_stride (elements); h bf16 [N][H] with
+ *       row stride h_stride.  H % 8 == 0, strides % 8 == 0, pointers 16-byte
+ *       aligned.
+ */
+int t2t_swiglu(const void *gu, int64_t gu_stride, void *h, int64_t h_stride, int32_t N,
+               int32_t H, void *stream);
+
+/*
+ * Gradient of t2t_swiglu with s = sigmoid(g): dg = dh u s (1 + g (1 - s)),
+ * du = dh g s, written as one [N][2H] buffer [dg | du] (the gate / up
+ * product's gradient).  Same layout rules as t2t_swiglu.
+ */
+int t2t_swiglu_backward(const void *gu, int64_t gu_stride, const void *dh, int64_t dh_stride,
+                        void *dgu, int64_t dgu_stride, int32_t N, int32_t H, void *stream);
+
+/*
  * Cross-entropy rows of a linear head: loss and logit gradient in one pass.
  * Replaces, per chunk of rows, torch's F.cross_entropy(logits.float(),
  * targets, ignore_index, reduction="sum") and its backward inside the

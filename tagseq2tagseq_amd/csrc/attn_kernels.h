@@ -116,6 +116,12 @@ hipError_t launch_attn_decode(const TensorView& q, const TensorView& k, const Te
                               int B, int Hq, int Hkv, int Tq, int Tkv, int D, float scale,
                               float* workspace, hipStream_t stream);
 
+// SwiGLU: h = silu(g) u from [g | u] rows, and [dg | du] from dh.
+hipError_t launch_swiglu_fwd(const __bf16* gu, int64_t gs, __bf16* h, int64_t hs, int N, int H,
+                             hipStream_t stream);
+hipError_t launch_swiglu_bwd(const __bf16* gu, int64_t gs, const __bf16* dh, int64_t dhs,
+                             __bf16* dgu, int64_t dgs, int N, int H, hipStream_t stream);
+
 // Cross-entropy rows: loss and (softmax - onehot) * scale per bf16 row.
 hipError_t launch_ce_rows(const uint16_t* logits, uint16_t* grad, int64_t rows, int V, int64_t ld,
                           const int64_t* target, int64_t ignore_index, const float* scale,

@@ -504,6 +504,53 @@ int t2t_rms_norm(const void* x, int64_t x_stride, const void* weight, int32_t we
                     "t2t_rms_norm launch");
 }
 
+namespace {
+
+int check_swiglu(int32_t N, int32_t H, const void* const* ptrs, int np, const int64_t* strides,
+                 int ns, const int64_t* min_strides) {
+  if (N < 0 || H <= 0 || H % 8 != 0)
+    return fail(T2T_EINVAL, "N=%d H=%d: need H > 0, H %% 8 == 0", N, H);
+  for (int i = 0; i < np; ++i) {
+    if (!ptrs[i]) return fail(T2T_EINVAL, "NULL buffer");
+    if (reinterpret_cast<uintptr_t>(ptrs[i]) & 15)
+      return fail(T2T_EINVAL, "buffers must be 16-byte aligned");
+  }
+  for (int i = 0; i < ns; ++i)
+    if (strides[i] % 8 != 0 || strides[i] < min_strides[i])
+      return fail(T2T_EINVAL, "row stride %lld (need a multiple of 8, >= %lld)",
+                  (long long)strides[i], (long long)min_strides[i]);
+  return T2T_OK;
+}
+
+}  // namespace
+
+int t2t_swiglu(const void* gu, int64_t gu_stride, void* h, int64_t h_stride, int32_t N, int32_t H,
+               void* stream) {
+  const void* ptrs[] = {gu, h};
+  const int64_t strides[] = {gu_stride, h_stride};
+  const int64_t mins[] = {2 * (int64_t)H, H};
+  const int rc = check_swiglu(N, H, ptrs, 2, strides, 2, mins);
+  if (rc) return rc;
+  return hip_status(t2t::launch_swiglu_fwd(static_cast<const __bf16*>(gu), gu_stride,
+                                           static_cast<__bf16*>(h), h_stride, N, H,
+                                           static_cast<hipStream_t>(stream)),
+                    "t2t_swiglu launch");
+}
+
+int t2t_swiglu_backward(const void* gu, int64_t gu_stride, const void* dh, int64_t dh_stride,
+                        void* dgu, int64_t dgu_stride, int32_t N, int32_t H, void* stream) {
+  const void* ptrs[] = {gu, dh, dgu};
+  const int64_t strides[] = {gu_stride, dh_stride, dgu_stride};
+  const int64_t mins[] = {2 * (int64_t)H, H, 2 * (int64_t)H};
+  const int rc = check_swiglu(N, H, ptrs, 3, strides, 3, mins);
+  if (rc) return rc;
+  return hip_status(t2t::launch_swiglu_bwd(static_cast<const __bf16*>(gu), gu_stride,
+                                           static_cast<const __bf16*>(dh), dh_stride,
+                                           static_cast<__bf16*>(dgu), dgu_stride, N, H,
+                                           static_cast<hipStream_t>(stream)),
+                    "t2t_swiglu_backward launch");
+}
+
 int t2t_ce_rows(const void* logits, void* grad, int64_t rows, int32_t V, int64_t ld,
                 const int64_t* target, int64_t ignore_index, const float* scale, float* row_loss,
                 void* stream) {

@@ -30,6 +30,7 @@ import torch.utils.checkpoint
 
 from . import norm
 from .attention import FlexSelfAttention
+from .glu import SwiGLUFn, swiglu_applies
 from .head_loss import HeadCEFn, fused_head_applies
 
 
@@ -52,7 +53,8 @@ class RMSNorm(nn.Module):
 
 
 class GLU(nn.Module):
-    """Gated linear unit: out(act(gate(x)) * up(x)) (SwiGLU for silu)."""
+    """Gated linear unit: out(act(gate(x)) * up(x)) (SwiGLU for silu; bf16 rows
+    on the GPU run the fused SwiGLU kernels of ``glu``)."""
 
     def __init__(self, in_dim: int, out_dim: int, hidden_dim: int, activation: str = "silu",
                  dropout: float = 0.0, fp8: bool = False):
@@ -63,7 +65,11 @@ class GLU(nn.Module):
         self.dropout = nn.Dropout(dropout)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        g, u = self.gate_up(x).chunk(2, dim=-1)
+        gu = self.gate_up(x)
+        if self.act is F.silu and swiglu_applies(gu):
+            # one fused pass each way (t2t_swiglu), the gradient of [g | u] whole
+            return self.dropout(self.down(SwiGLUFn.apply(gu)))
+        g, u = gu.chunk(2, dim=-1)
         return self.dropout(self.down(self.act(g) * u))
 
 

@@ -329,3 +329,14 @@ def test_ce_rows_argument_checks():
     assert lib.t2t_ce_rows(*args(sc=None)) == -1 and "NULL" in _err()
     assert lib.t2t_ce_rows(*args(lg=ctypes.c_void_p(0x1002))) == -1 and "aligned" in _err()
     assert lib.t2t_ce_rows(*args(rows=0)) == 0
+
+
+def test_swiglu_argument_checks():
+    lib = _lib.lib()
+    P = ctypes.c_void_p(0x1000)
+    assert lib.t2t_swiglu(P, 32, P, 16, 4, 12, None) == -1 and "H" in _err()
+    assert lib.t2t_swiglu(P, 24, P, 16, 4, 16, None) == -1 and "stride" in _err()
+    assert lib.t2t_swiglu(None, 32, P, 16, 4, 16, None) == -1 and "NULL" in _err()
+    assert lib.t2t_swiglu(ctypes.c_void_p(0x1008), 32, P, 16, 4, 16, None) == -1
+    assert lib.t2t_swiglu_backward(P, 32, P, 8, P, 32, 4, 16, None) == -1 and "stride" in _err()
+    assert lib.t2t_swiglu(P, 32, P, 16, 0, 16, None) == 0
