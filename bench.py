@@ -688,30 +688,15 @@ def backbone_step(args, dev):
     span / link lists, embedding, 12 layers, RMSNorm, tied linear + CE loss,
     backward, AdamW) of the 12-layer d768 H12 (D 64) backbone on a packed
     T = 16384 row of random token ids with the configs[2] cross_doc_link
-    generator; random-init weights.  Prints one JSON line (tokens/s)."""
-    from tagseq2tagseq_amd.modules import TS2TSTrainingModule
-    T, V = 16384, 50257
-    row = synth.config_rows(3, seed=args.seed)[0]
-    lists = TokenLists(T, [row.spans], dev, words=row.words, link_rows=[row.link_rows])
-
-    def creator(tokens, **kw):
-        return build_block_mask(*lists.build())
-
-    torch.manual_seed(args.seed)
-    model = TS2TSTrainingModule.from_config(
-        vocab_size=V, num_layers=12, model_dim=768, num_heads=12, max_seq_len=T, dropout=0.0,
-        drop_path_rate=0.0, block_mask_creator=creator).to(dev, torch.bfloat16)
-    opt = torch.optim.AdamW(model.parameters(), lr=1e-4, foreach=True)
-    g = torch.Generator().manual_seed(args.seed)
-    tokens = torch.randint(0, V, (1, T + 1), generator=g).to(dev)
-    batch = {"tokens": tokens}
-
-    def step():
-        loss = model(batch)
-        loss.backward()
-        opt.step()
-        opt.zero_grad(set_to_none=True)
-        return loss
+    generator; random-init weights (tagseq2tagseq_amd.train_step).  The
+    library products use the committed TunableOp selections
+    (tagseq2tagseq_amd.gemm_tuning) when this software stack matches them.
+    Prints one JSON line (tokens/s)."""
+    from tagseq2tagseq_amd.gemm_tuning import TUNED_FILE, use_tuned_gemms
+    from tagseq2tagseq_amd.train_step import VOCAB, configs4_step
+    tuned = False if args.no_gemm_tuning else use_tuned_gemms()
+    step = configs4_step(dev, seed=args.seed)
+    model, row, T, V = step.model, step.row, step.T, VOCAB
 
     for _ in range(args.warmup):
         step()
@@ -735,6 +720,7 @@ def backbone_step(args, dev):
         "config": {"workload": "12-layer backbone training step (configs[4])", "T": T,
                    "vocab": V, "params": n_params, "n_docs": row.n_docs,
                    "optimizer": "AdamW (foreach)"},
+        "gemm_tuning": {"file": os.path.relpath(TUNED_FILE, ROOT), "loaded": tuned},
         "final_loss": round(float(loss.item()), 4),
         "prologue": prologue,
     }))
@@ -743,6 +729,9 @@ def backbone_step(args, dev):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--no-gemm-tuning", action="store_true",
+                    help="with --config 5: the library products' default heuristics instead of "
+                         "the committed TunableOp selections")
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", type=int, default=3, choices=[1, 2, 3, 4, 5],

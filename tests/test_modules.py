@@ -146,3 +146,16 @@ def test_model_weights_state_tracks_edits_and_mode():
     assert m._weights_state() != s2
     m.eval()
     assert m._weights_state() == s2
+
+
+def test_gemm_tuning_file_has_validators_and_gfx950_shapes():
+    from tagseq2tagseq_amd import gemm_tuning
+    lines = open(gemm_tuning.TUNED_FILE).read().splitlines()
+    validators = {l.split(",")[1] for l in lines if l.startswith("Validator,")}
+    assert {"PT_VERSION", "HIP_VERSION", "HIPBLASLT_VERSION", "GCN_ARCH_NAME"} <= validators
+    assert any("gfx950" in l for l in lines if l.startswith("Validator,GCN_ARCH_NAME"))
+    shapes = [l.split(",")[1] for l in lines if l.startswith("GemmTunableOp")]
+    # the head (vocabulary padded to 50264) and the four layer projections
+    assert any("50264" in s for s in shapes) and len(shapes) >= 10
+    if not torch.cuda.is_available():
+        assert gemm_tuning.use_tuned_gemms() is False
