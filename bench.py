@@ -719,7 +719,7 @@ def backbone_step(args, dev):
         "data": "synthetic (random token ids, seeded packed documents)",
         "config": {"workload": "12-layer backbone training step (configs[4])", "T": T,
                    "vocab": V, "params": n_params, "n_docs": row.n_docs,
-                   "optimizer": "AdamW (foreach)"},
+                   "optimizer": "AdamW (fused)"},
         "gemm_tuning": {"file": os.path.relpath(TUNED_FILE, ROOT), "loaded": tuned},
         "final_loss": round(float(loss.item()), 4),
         "prologue": prologue,

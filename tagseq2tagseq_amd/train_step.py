@@ -28,7 +28,9 @@ def configs4_step(dev: torch.device, seed: int = 0):
     model = TS2TSTrainingModule.from_config(
         vocab_size=VOCAB, num_layers=LAYERS, model_dim=DIM, num_heads=HEADS, max_seq_len=T,
         dropout=0.0, drop_path_rate=0.0, block_mask_creator=creator).to(dev, torch.bfloat16)
-    opt = torch.optim.AdamW(model.parameters(), lr=1e-4, foreach=True)
+    # the fused form: one kernel per parameter group step (-1.1 ms per step
+    # against the foreach form at configs[4])
+    opt = torch.optim.AdamW(model.parameters(), lr=1e-4, fused=True)
     g = torch.Generator().manual_seed(seed)
     batch = {"tokens": torch.randint(0, VOCAB, (1, T + 1), generator=g).to(dev)}
 
