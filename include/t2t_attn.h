@@ -392,6 +392,27 @@ int t2t_first_input_diff(const int64_t *tokens_a, const int64_t *tokens_b, const
                          int32_t *out, void *stream);
 
 /*
+ * Weight gradient of a linear map over many rows: C[m][n] = sum over k of
+ * A[k][m] B[k][n], i.e. dW = dY^T X for y = x W^T with dY [K][M] and X [K][N].
+ * Replaces the weight-gradient product of nn.Linear's backward for the
+ * layers' projections (tunalab FlexSelfAttention's qkv / out projections and
+ * GLU's gate_up / down, called from model/modules/layer.py:33-35), which
+ * torch runs as one library product with only (M / 128) (N / 128) output
+ * tiles.  K is split across work-groups into fp32 partials (the workspace),
+ * summed in a fixed order by a second launch: deterministic, no atomics.
+ *   a, b     bf16 row-major with row strides lda, ldb (elements, % 8 == 0,
+ *            >= M / >= N), 16-byte aligned.
+ *   out      [M][N] row-major, out_dtype T2T_DTYPE_BF16 or T2T_DTYPE_F32.
+ *   M, N     multiples of 128; K a multiple of 64 (T2T_EUNSUPPORTED otherwise).
+ *   workspace  t2t_wgrad_workspace(M, N, K) bytes, 16-byte aligned.
+ */
+int64_t t2t_wgrad_workspace(int32_t M, int32_t N, int32_t K);
+
+int t2t_wgrad(const void *a, int64_t lda, const void *b, int64_t ldb, void *out,
+              int32_t out_dtype, int32_t M, int32_t N, int32_t K, void *workspace,
+              int64_t workspace_bytes, void *stream);
+
+/*
  * SwiGLU of the MLP: h = silu(g) * u, computed in fp32 and rounded once, from
  * the gate / up product's rows [g | u] (g = the first H columns, u = the next
  * H).  Replaces the activation and product inside tunalab's GLU

@@ -62,6 +62,8 @@ _SIGS = {
     "t2t_attn_decode_workspace": ([_I32] * 5, ctypes.c_int64),
     "t2t_rms_norm": ([_P, _I64, _P, _I32, _P, _I64, _P, _I32, _I32, ctypes.c_float, _P],
                      ctypes.c_int),
+    "t2t_wgrad_workspace": ([_I32, _I32, _I32], ctypes.c_int64),
+    "t2t_wgrad": ([_P, _I64, _P, _I64, _P, _I32, _I32, _I32, _I32, _P, _I64, _P], _I32),
     "t2t_swiglu": ([_P, _I64, _P, _I64, _I32, _I32, _P], _I32),
     "t2t_swiglu_backward": ([_P, _I64, _P, _I64, _P, _I64, _I32, _I32, _P], _I32),
     "t2t_ce_rows": ([_P, _P, _I64, _I32, _I64, _P, _I64, _P, _P, _P], _I32),

@@ -36,6 +36,7 @@ from . import _lib
 from typing import List, Tuple
 
 from .block_mask import T2TBlockMask, from_torch_block_mask, tables_c_struct
+from .linear import Linear
 
 LN2 = math.log(2.0)
 _DTYPE_CODES = {torch.bfloat16: _lib.T2T_DTYPE_BF16, torch.float32: _lib.T2T_DTYPE_F32}
@@ -357,8 +358,8 @@ class FlexSelfAttention(nn.Module):
         self.dim = dim
         self.num_heads = num_heads
         self.head_dim = dim // num_heads
-        self.qkv = nn.Linear(dim, 3 * dim, bias=False)
-        self.proj = nn.Linear(dim, dim, bias=False)
+        self.qkv = Linear(dim, 3 * dim, bias=False)
+        self.proj = Linear(dim, dim, bias=False)
         self.rotary = Rotary(self.head_dim, max_seq_len)
         self.fp8_out_proj = fp8_out_proj
         if fp8_out_proj:

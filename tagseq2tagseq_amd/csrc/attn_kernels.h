@@ -116,6 +116,11 @@ hipError_t launch_attn_decode(const TensorView& q, const TensorView& k, const Te
                               int B, int Hq, int Hkv, int Tq, int Tkv, int D, float scale,
                               float* workspace, hipStream_t stream);
 
+// Weight gradient C = A^T B over K rows (split-K, fp32 partials summed in order).
+int wgrad_splits(int M, int N, int K);
+hipError_t launch_wgrad(const __bf16* a, int64_t lda, const __bf16* b, int64_t ldb, float* part,
+                        void* out, bool out_f32, int M, int N, int K, hipStream_t stream);
+
 // SwiGLU: h = silu(g) u from [g | u] rows, and [dg | du] from dh.
 hipError_t launch_swiglu_fwd(const __bf16* gu, int64_t gs, __bf16* h, int64_t hs, int N, int H,
                              hipStream_t stream);

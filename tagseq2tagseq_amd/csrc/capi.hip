@@ -504,6 +504,39 @@ int t2t_rms_norm(const void* x, int64_t x_stride, const void* weight, int32_t we
                     "t2t_rms_norm launch");
 }
 
+int64_t t2t_wgrad_workspace(int32_t M, int32_t N, int32_t K) {
+  if (M <= 0 || N <= 0 || K <= 0 || M % 128 || N % 128 || K % 64) return 0;
+  return (int64_t)t2t::wgrad_splits(M, N, K) * M * N * 4;
+}
+
+int t2t_wgrad(const void* a, int64_t lda, const void* b, int64_t ldb, void* out,
+              int32_t out_dtype, int32_t M, int32_t N, int32_t K, void* workspace,
+              int64_t workspace_bytes, void* stream) {
+  if (M <= 0 || N <= 0 || K <= 0) return fail(T2T_EINVAL, "M=%d N=%d K=%d", M, N, K);
+  if (M % 128 || N % 128 || K % 64)
+    return fail(T2T_EUNSUPPORTED, "M=%d N=%d K=%d: need M, N multiples of 128 and K of 64", M,
+                N, K);
+  if (out_dtype != T2T_DTYPE_BF16 && out_dtype != T2T_DTYPE_F32)
+    return fail(T2T_EINVAL, "out_dtype=%d", out_dtype);
+  if (!a || !b || !out || !workspace) return fail(T2T_EINVAL, "a / b / out / workspace is NULL");
+  if ((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b) |
+       reinterpret_cast<uintptr_t>(out) | reinterpret_cast<uintptr_t>(workspace)) & 15)
+    return fail(T2T_EINVAL, "buffers must be 16-byte aligned");
+  if (lda % 8 || ldb % 8 || lda < M || ldb < N)
+    return fail(T2T_EINVAL, "lda=%lld ldb=%lld: need multiples of 8, >= M / N", (long long)lda,
+                (long long)ldb);
+  const int64_t need = t2t_wgrad_workspace(M, N, K);
+  if (workspace_bytes < need)
+    return fail(T2T_EINVAL, "workspace of %lld bytes, %lld needed", (long long)workspace_bytes,
+                (long long)need);
+  return hip_status(t2t::launch_wgrad(static_cast<const __bf16*>(a), lda,
+                                      static_cast<const __bf16*>(b), ldb,
+                                      static_cast<float*>(workspace), out,
+                                      out_dtype == T2T_DTYPE_F32, M, N, K,
+                                      static_cast<hipStream_t>(stream)),
+                    "t2t_wgrad launch");
+}
+
 namespace {
 
 int check_swiglu(int32_t N, int32_t H, const void* const* ptrs, int np, const int64_t* strides,

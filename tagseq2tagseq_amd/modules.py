@@ -32,6 +32,7 @@ from . import norm
 from .attention import FlexSelfAttention
 from .glu import SwiGLUFn, swiglu_applies
 from .head_loss import HeadCEFn, fused_head_applies
+from .linear import Linear
 
 
 class RMSNorm(nn.Module):
@@ -59,8 +60,8 @@ class GLU(nn.Module):
     def __init__(self, in_dim: int, out_dim: int, hidden_dim: int, activation: str = "silu",
                  dropout: float = 0.0, fp8: bool = False):
         super().__init__()
-        self.gate_up = nn.Linear(in_dim, 2 * hidden_dim, bias=False)
-        self.down = nn.Linear(hidden_dim, out_dim, bias=False)
+        self.gate_up = Linear(in_dim, 2 * hidden_dim, bias=False)
+        self.down = Linear(hidden_dim, out_dim, bias=False)
         self.act = {"silu": F.silu, "gelu": F.gelu, "relu": F.relu}[activation]
         self.dropout = nn.Dropout(dropout)
 

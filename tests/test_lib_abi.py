@@ -340,3 +340,20 @@ def test_swiglu_argument_checks():
     assert lib.t2t_swiglu(ctypes.c_void_p(0x1008), 32, P, 16, 4, 16, None) == -1
     assert lib.t2t_swiglu_backward(P, 32, P, 8, P, 32, 4, 16, None) == -1 and "stride" in _err()
     assert lib.t2t_swiglu(P, 32, P, 16, 0, 16, None) == 0
+
+
+def test_wgrad_argument_checks():
+    lib = _lib.lib()
+    P = ctypes.c_void_p(0x1000)
+    ws = lib.t2t_wgrad_workspace(768, 768, 16384)
+    assert ws > 0 and ws % (768 * 768 * 4) == 0
+    assert lib.t2t_wgrad_workspace(100, 768, 64) == 0
+    assert lib.t2t_wgrad_workspace(128, 128, 32) == 0
+    args = lambda M=128, N=128, K=64, lda=128, ldb=128, dt=0, ws=1 << 20, a=P: (  # noqa: E731
+        a, lda, P, ldb, P, dt, M, N, K, P, ws, None)
+    assert lib.t2t_wgrad(*args(M=100)) == -2 and "128" in _err()
+    assert lib.t2t_wgrad(*args(K=96)) == -2
+    assert lib.t2t_wgrad(*args(dt=3)) == -1
+    assert lib.t2t_wgrad(*args(lda=120)) == -1 and "lda" in _err()
+    assert lib.t2t_wgrad(*args(ws=16)) == -1 and "workspace" in _err()
+    assert lib.t2t_wgrad(*args(a=None)) == -1 and "NULL" in _err()
