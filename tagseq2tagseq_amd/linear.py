@@ -83,7 +83,9 @@ class Linear(nn.Linear):
     GPU take their weight gradient from t2t_wgrad."""
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
+        # (graphs being compiled keep torch's own linear: the Function's
+        # backward calls the library through ctypes)
         if (self.bias is None and x.is_cuda and x.dtype == torch.bfloat16
-                and self.weight.dtype == torch.bfloat16):
+                and self.weight.dtype == torch.bfloat16 and not torch.compiler.is_compiling()):
             return WGradLinearFn.apply(x, self.weight)
         return super().forward(x)

@@ -67,7 +67,7 @@ class GLU(nn.Module):
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         gu = self.gate_up(x)
-        if self.act is F.silu and swiglu_applies(gu):
+        if self.act is F.silu and swiglu_applies(gu) and not torch.compiler.is_compiling():
             # one fused pass each way (t2t_swiglu), the gradient of [g | u] whole
             return self.dropout(self.down(SwiGLUFn.apply(gu)))
         g, u = gu.chunk(2, dim=-1)
@@ -164,7 +164,7 @@ class LinearCELoss(nn.Module):
     def forward(self, x: torch.Tensor, targets: torch.Tensor) -> torch.Tensor:
         x = x.reshape(-1, x.shape[-1])
         t = targets.reshape(-1)
-        if fused_head_applies(x, self.weight):
+        if fused_head_applies(x, self.weight) and not torch.compiler.is_compiling():
             return HeadCEFn.apply(x, self.weight, t, int(self.ignore_index), self.gpu_chunk)
         n = (t != self.ignore_index).sum().clamp(min=1)
         total = x.new_zeros((), dtype=torch.float32)
