@@ -138,3 +138,15 @@ def test_module_uses_fused_path_and_matches_cpu_chunks():
     gpu = head(x.to(DEV), t.to(DEV))
     assert gpu.grad_fn is not None and type(gpu.grad_fn).__name__ == "HeadCEFnBackward"
     torch.testing.assert_close(gpu.cpu(), cpu, rtol=5e-3, atol=5e-3)
+
+
+def test_head_loss_takes_host_targets_and_checks_shapes():
+    x = torch.randn(16, 64, device=DEV).to(torch.bfloat16)
+    w = torch.randn(40, 64, device=DEV)
+    t = torch.randint(0, 40, (16,))  # host tensor: moved to the rows' device
+    ref = F.cross_entropy(F.linear(x, w.to(torch.bfloat16)).float(), t.to(DEV))
+    torch.testing.assert_close(head_cross_entropy(x, w, t), ref, rtol=1e-5, atol=1e-5)
+    with pytest.raises(ValueError):
+        head_cross_entropy(x, w, t[:15])
+    with pytest.raises(ValueError):
+        head_cross_entropy(x, torch.randn(40, 32, device=DEV), t)
