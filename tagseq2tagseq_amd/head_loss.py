@@ -55,13 +55,13 @@ class HeadCEFn(torch.autograd.Function):
         V = weight.shape[0]
         ld = (V + 7) // 8 * 8
         dev = x.device
-        w = torch.zeros((ld, D), dtype=torch.bfloat16, device=dev)
-        w[:V].copy_(weight)
         t = targets.reshape(-1).to(device=dev, dtype=torch.int64).contiguous()
         if t.numel() != N:
             raise ValueError(f"{t.numel()} targets for {N} rows")
         if weight.shape[1] != D:
             raise ValueError(f"weight {tuple(weight.shape)} does not match rows of width {D}")
+        w = torch.zeros((ld, D), dtype=torch.bfloat16, device=dev)
+        w[:V].copy_(weight)
         n = (t != ignore_index).sum().clamp(min=1)
         scale = (1.0 / n.to(torch.float32)).reshape(1)
         row_loss = torch.empty((N,), dtype=torch.float32, device=dev)
