@@ -125,6 +125,7 @@ class TS2TSModel:
         self.fuse_rows = True  # few-row steps on the fused row kernels (rows.py)
         self._graph: Optional[_DecodeGraph] = None
         self._weights_seen = None  # _weights_state() the cache was filled under
+        self._param_slots = None   # (module, name) of every backbone / norm parameter
 
     @classmethod
     def from_config(cls, vocab_size: int, num_layers: int, model_dim: int, num_heads: int,
@@ -168,15 +169,25 @@ class TS2TSModel:
         self.kv_cache = None
         self._graph = None
         self._weights_seen = None
+        self._param_slots = None
 
     def _weights_state(self):
         """What the cached keys / values depend on besides the inputs: the mode
         and, per parameter, its storage address and version counter (bumped by
         every in-place write through the parameter, optimizer steps and
-        load_state_dict included)."""
-        params = (*self.backbone.parameters(), *self.norm.parameters(), self.embedding_weight,
-                  self.lm_head_weight)
-        return self.backbone.training, tuple((p.data_ptr(), p._version) for p in params)
+        load_state_dict included).  The (module, attribute) slots that hold
+        the parameters are listed once (walking the module tree per token cost
+        ~0.2 ms of host time before each step); each call reads the slots
+        again, so a parameter assigned anew is seen.  Submodules replaced
+        after the first cached call need reset_cache()."""
+        if self._param_slots is None:
+            self._param_slots = [(m, name) for owner in (self.backbone, self.norm)
+                                 for m in owner.modules()
+                                 for name, prm in m._parameters.items() if prm is not None]
+        params = [m._parameters.get(name) for m, name in self._param_slots]
+        params += (self.embedding_weight, self.lm_head_weight)
+        return self.backbone.training, tuple(None if p is None else (p.data_ptr(), p._version)
+                                             for p in params)
 
     @torch.no_grad()
     def forward_inference(self, tokens: torch.Tensor, doc_spans: Optional[List[Any]] = None,

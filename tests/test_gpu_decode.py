@@ -291,8 +291,8 @@ def test_fused_row_kernels_match_unfused_layers(graphs, dim, heads, layers, monk
 @pytest.mark.parametrize("graphs", [True, False])
 def test_cache_dropped_when_weights_change(graphs):
     """The cached keys / values and the captured step are rebuilt after an
-    in-place weight edit, load_state_dict, an optimizer step and a train() /
-    eval() switch: each following call equals the full recompute under the
+    in-place weight edit, load_state_dict, an optimizer step, a train() /
+    eval() switch and a parameter assigned anew: each following call equals the full recompute under the
     new weights (the reference recomputes every call, model/model.py:214-237)."""
     m = _model(create_doc_causal_block_mask)
     m.use_graphs = graphs
@@ -323,6 +323,9 @@ def test_cache_dropped_when_weights_change(graphs):
     m.train()
     m.eval()
     step("after train() / eval()")
+    down = m.backbone.layers[0].mlp.down
+    down.weight = torch.nn.Parameter(down.weight.detach() * 1.1)
+    step("after a parameter is assigned anew")
 
 
 @pytest.mark.parametrize("words", [0, 1, 3])
