@@ -32,7 +32,7 @@ def _ce_rows(logits, V, target, ignore, scale, grad=None):
 
 
 @pytest.mark.parametrize("rows,V,ld", [(5, 1, 8), (33, 1000, 1000), (64, 1003, 1008),
-                                       (17, 50257, 50264)])
+                                       (17, 50257, 50264), (3, 70001, 70008)])
 def test_ce_rows_against_float64(rows, V, ld):
     g = torch.Generator().manual_seed(rows + V)
     x = (torch.randn(rows, ld, generator=g) * 3).to(torch.bfloat16).to(DEV)
