@@ -111,6 +111,62 @@ def profile_mfma_busy(config: int):
     return {"source": os.path.relpath(path, ROOT), **got} if got else None
 
 
+def executed_work(bm, B: int, Hq: int, D: int, n_pairs: int, config: int):
+    """MFMA work the attention kernels execute for one step, counted from the
+    block mask, against the useful work of the metric.
+
+    The kernels compute whole MFMA blocks: the forward a 32-query x 64-key
+    unit of a non-skip tile when any pair in it is allowed (D / 4 MFMAs: the
+    scores and P V), dK/dV and dQ a 32 x 32 block when any pair in it is
+    allowed (D / 4 MFMAs: S, dP, dV, dK; 3 D / 16: S, dP, dQ).  An MFMA
+    (32 x 32 x 16) is 32768 FLOP.  Useful work is 4 D (forward), 8 D (dK/dV,
+    which recomputes S and dP) and 6 D (dQ, the same recompute) FLOP per
+    allowed pair, and 14 D per pair for the step (the metric's convention,
+    S and dP once).  `busy_needed_for_50pct`: the share of the chip's MFMA
+    cycles (at the 2.4 GHz of the published peak) the executed work would
+    have to fill for the step to reach 50 % of peak on useful FLOPs, were
+    the step nothing but these three kernels.  `profile_mfma` repeats the
+    per-dispatch MFMA counts of the committed instruction-mix summary, which
+    come from the counters (SQ_INSTS_MFMA) of a profiled run of this bench."""
+    tc = bm.tile_class
+    Bm, nt = tc.shape[0], tc.shape[-1]
+    rows_per_mask = B // Bm if Bm < B else 1
+    n_full = int((tc == 2).sum())
+    # row-major bitmaps of the partial tiles: [P, 128 queries, 4 words of 32 keys]
+    b_, r_, c_ = (tc == 1).nonzero(as_tuple=True)
+    slots = (bm.kv_bits_off[b_, r_].to(torch.int64) + c_.to(torch.int64))
+    words = bm.tile_bits[slots, 0] != 0 if slots.numel() else torch.zeros(
+        (0, 128, 4), dtype=torch.bool, device=tc.device)
+    blocks32 = words.view(-1, 4, 32, 4).any(2)                        # [P, q blk, k blk]
+    units_fwd = words.view(-1, 4, 32, 2, 2).any(4).any(2)             # [P, q blk, k half]
+    n_blk = (16 * n_full + int(blocks32.sum())) * rows_per_mask * Hq
+    n_fwd = (8 * n_full + int(units_fwd.sum())) * rows_per_mask * Hq
+    mf = {"attn_fwd_bf16_kernel": n_fwd * D // 4,
+          "bwd_dkdv_kernel": n_blk * D // 4,
+          "bwd_dq_kernel": n_blk * 3 * D // 16}
+    useful = {"attn_fwd_bf16_kernel": 4.0, "bwd_dkdv_kernel": 8.0, "bwd_dq_kernel": 6.0}
+    out = {}
+    executed = 0.0
+    for k, n in mf.items():
+        fl = 32768.0 * n
+        executed += fl
+        out[k] = {"mfma_per_launch": int(n), "executed_gflop": round(fl / 1e9, 2),
+                  "executed_over_useful": round(fl / (useful[k] * D * n_pairs * Hq), 4)}
+    step_useful = 14.0 * D * n_pairs * Hq
+    out["step"] = {"executed_gflop": round(executed / 1e9, 2),
+                   "useful_gflop": round(step_useful / 1e9, 2),
+                   "executed_over_useful": round(executed / step_useful, 4),
+                   "busy_needed_for_50pct": round(0.5 * executed / step_useful, 4),
+                   "allowed_share_fwd_units": round(n_pairs * Hq / (2048.0 * n_fwd), 4),
+                   "allowed_share_bwd_blocks": round(n_pairs * Hq / (1024.0 * n_blk), 4)}
+    from tagseq2tagseq_amd.rocprof_summary import read_mfma_counts
+    path = os.path.join(ROOT, "profiles", f"instruction_mix_config{config}.txt")
+    prof = {k: v for k, v in read_mfma_counts(path).items() if k in mf}
+    if prof:
+        out["profile_mfma"] = {"source": os.path.relpath(path, ROOT), **prof}
+    return out
+
+
 def time_launches(fn, reps: int) -> float:
     """Mean duration (ms) of fn()'s launches, HIP events on the current stream."""
     start = torch.cuda.Event(enable_timing=True)
@@ -481,7 +537,7 @@ def decode_bench(args, dev):
     else:
         def run_reps():
             for _ in range(args.reps):
-                L.t2t_attn_decode(*call_args)
+                _lib.check(L.t2t_attn_decode(*call_args), "t2t_attn_decode")
     run_reps()
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -949,6 +1005,7 @@ def main():
             "traffic_source": f"profiles/hbm_traffic_config{args.config}.txt",
         },
         "mfma_busy": profile_mfma_busy(args.config),
+        "executed_work": executed_work(bm, B, Hq, D, n_pairs, args.config),
         "clock": clock,
         "kernels_ms": {
             "token_inputs_kernel": round(t_tok, 4),

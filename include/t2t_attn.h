@@ -67,15 +67,19 @@ typedef struct t2t_tensor {
  *       ascending index (longest first for load balance, neighbours back to
  *       back for cache reuse of the tiles they share);
  *   kv_bits_off int32[Bm][nt]: bitmap slots of a tile row: partial tile
- *       (r, c) uses slot kv_bits_off[r] + c (t2t_mask_meta writes
- *       b nt (nt + 1) / 2 + r (r + 1) / 2, the tile's position in the lower
- *       triangle);
+ *       (r, c) uses slot kv_bits_off[r] + c, and distinct partial tiles must
+ *       get distinct slots.  t2t_mask_meta writes b nt (nt + 1) / 2 +
+ *       r (r + 1) / 2, the tile's position in the lower triangle, which is
+ *       distinct only because its masks are causal (every partial tile has
+ *       c <= r); a caller filling the tables for a mask with partial tiles
+ *       above the diagonal uses b nt^2 + r nt (one slot per tile);
  *   q_bits_slot int32[Bm][nt][nt]: bitmap slot of the i-th partial tile of a
  *       column (entries past q_num unspecified);
  *   tile_bits uint32[tile_bits_slots][2][128][4]: per partial tile, the
  *       allowed pairs as bits -- [0][q][w] bit j = allowed(q0 + q, k0 + 32 w + j),
  *       [1][k][w] bit j = allowed(q0 + 32 w + j, k0 + k);
- *   tile_bits_slots: capacity; Bm * nt * (nt + 1) / 2 always suffices.
+ *   tile_bits_slots: capacity; Bm * nt * (nt + 1) / 2 always suffices for
+ *       t2t_mask_meta's layout (Bm * nt * nt for the square one).
  */
 typedef struct t2t_block_mask {
   int32_t mask_batch; /* Bm */

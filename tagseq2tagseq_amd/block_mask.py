@@ -268,6 +268,8 @@ def from_torch_block_mask(bm, tile_chunk: int = 256) -> T2TBlockMask:
     on the mask's device, and the allowed-pair bitmap of every partial tile is
     evaluated from ``bm.mask_mod`` at head 0 over the tile's valid positions
     (positions past the sequence are masked, as create_block_mask pads).
+    Masks with partial tiles above the diagonal (not causal) are accepted:
+    their bitmaps take one slot per tile of the square.
     Requires 128 x 128 tiles, equal query and key lengths and one mask for
     every head (a head dimension of 1)."""
     if tuple(bm.BLOCK_SIZE) != (TILE, TILE):
@@ -304,11 +306,17 @@ def from_torch_block_mask(bm, tile_chunk: int = 256) -> T2TBlockMask:
     fq_num, fq_idx = _ordered(full.transpose(1, 2))
     row_order = _launch_order(kv_num + fkv_num, True)
     col_order = _launch_order(q_num + fq_num, False)
-    # bitmap slot of tile (b, r, c): b nt (nt + 1) / 2 + r (r + 1) / 2 + c, a
-    # fixed position in the lower triangle (the metadata pass's layout)
-    tri = nt * (nt + 1) // 2
-    kv_bits_off = (torch.arange(Bm, device=dev)[:, None] * tri
-                   + ar * (ar + 1) // 2).to(torch.int32)
+    # bitmap slot of partial tile (b, r, c): kv_bits_off[b, r] + c.  A causal
+    # mask has partial tiles on or below the diagonal only (c <= r), and the
+    # slots are the tile's position in the lower triangle, b nt (nt + 1) / 2 +
+    # r (r + 1) / 2 + c (the metadata pass's layout).  Any other mask (a
+    # bidirectional or sliding-window mask_mod, say) gets the square layout,
+    # b nt^2 + r nt + c, so that no two partial tiles share a slot.
+    upper = part & (ar[None, None, :] > ar[None, :, None])
+    per_row = nt * nt if bool(upper.any()) else nt * (nt + 1) // 2
+    row_start = ar * nt if per_row == nt * nt else ar * (ar + 1) // 2
+    kv_bits_off = (torch.arange(Bm, device=dev)[:, None] * per_row
+                   + row_start[None, :]).to(torch.int32)
     slot_grid = kv_bits_off[:, :, None].to(torch.int64) + ar[None, None, :]
     q_bits_slot = torch.gather(slot_grid.transpose(1, 2), 2, q_idx.to(torch.int64))
     q_bits_slot = torch.where(ar[None, None, :] < q_num[:, :, None], q_bits_slot,
@@ -316,7 +324,7 @@ def from_torch_block_mask(bm, tile_chunk: int = 256) -> T2TBlockMask:
     # bitmaps of the partial tiles
     pb, pr, pc = part.nonzero(as_tuple=True)
     P = int(pb.numel())
-    tile_bits = torch.zeros((max(1, Bm * tri), 2, TILE, 4), **i32)
+    tile_bits = torch.zeros((max(1, Bm * per_row), 2, TILE, 4), **i32)
     t = torch.arange(TILE, device=dev)
     for s0 in range(0, P, tile_chunk):
         b_, r_, c_ = (x[s0:s0 + tile_chunk] for x in (pb, pr, pc))

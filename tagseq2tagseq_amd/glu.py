@@ -21,8 +21,12 @@ def _stream(t: torch.Tensor) -> ctypes.c_void_p:
 
 
 def _rows(t: torch.Tensor) -> torch.Tensor:
+    """[N, C] rows as the kernels read them: unit column stride, rows 16-byte
+    aligned (row stride a multiple of 8 elements, 16-byte aligned start);
+    anything else is copied."""
     t = t.reshape(-1, t.shape[-1])
-    return t if t.stride(1) == 1 and t.stride(0) % 8 == 0 else t.contiguous()
+    ok = t.stride(1) == 1 and t.stride(0) % 8 == 0 and t.data_ptr() % 16 == 0
+    return t if ok else t.contiguous()
 
 
 def swiglu_applies(gu: torch.Tensor) -> bool:

@@ -31,7 +31,7 @@ import torch.utils.checkpoint
 from . import norm
 from .attention import FlexSelfAttention
 from .glu import SwiGLUFn, swiglu_applies
-from .head_loss import HeadCEFn, fused_head_applies
+from .head_loss import HeadCEFn, fused_head_applies, head_loss_needs_grad, head_loss_value
 from .linear import Linear
 
 
@@ -165,8 +165,12 @@ class LinearCELoss(nn.Module):
         x = x.reshape(-1, x.shape[-1])
         t = targets.reshape(-1)
         if fused_head_applies(x, self.weight) and not torch.compiler.is_compiling():
+            if not head_loss_needs_grad(x, self.weight):
+                return head_loss_value(x, self.weight, t, self.ignore_index, self.gpu_chunk)
             return HeadCEFn.apply(x, self.weight, t, int(self.ignore_index), self.gpu_chunk)
-        n = (t != self.ignore_index).sum().clamp(min=1)
+        # mean over the counted rows; 0 / 0 = NaN when every row is ignored,
+        # as torch's mean cross-entropy
+        n = (t != self.ignore_index).sum()
         total = x.new_zeros((), dtype=torch.float32)
         for r0 in range(0, x.shape[0], self.chunk):
             xs, ts = x[r0:r0 + self.chunk], t[r0:r0 + self.chunk]

@@ -234,6 +234,21 @@ def read_mfma_busy(path: str) -> Dict[str, float]:
     return out
 
 
+def read_mfma_counts(path: str) -> Dict[str, int]:
+    """MFMA instructions per dispatch, per kernel, from the table of an
+    `insts` summary (the first two columns: kernel, MFMA)."""
+    out: Dict[str, int] = {}
+    try:
+        with open(path) as f:
+            for line in f:
+                tok = line.split()
+                if len(tok) >= 2 and not line.startswith("#") and tok[1].isdigit():
+                    out[tok[0]] = int(tok[1])
+    except FileNotFoundError:
+        pass
+    return out
+
+
 def main(argv: List[str]) -> None:
     if len(argv) >= 4 and argv[0] == "trace":
         sys.stdout.write(trace(argv[1], argv[2], argv[3], " ".join(argv[4:])))

@@ -45,6 +45,26 @@ def test_swiglu_strided_rows_and_saturation():
     assert torch.isfinite(h).all()
 
 
+def test_swiglu_unaligned_view_is_copied():
+    """Rows whose stride is a multiple of 8 elements but whose first element
+    is not 16-byte aligned (a buffer viewed from its second element) take the
+    copy path, forward and backward, and match the float32 reference."""
+    g = torch.Generator().manual_seed(7)
+    buf = torch.randn(9 * 72 + 1, generator=g).to(torch.bfloat16).to(DEV)
+    gu0 = buf[1:].view(9, 72)[:, :64]  # starts 2 bytes past the allocation
+    assert gu0.stride(0) % 8 == 0 and gu0.data_ptr() % 16 != 0
+    dh = torch.randn(9, 32, generator=g).to(torch.bfloat16).to(DEV)
+    leaf = gu0.detach().requires_grad_()
+    h = swiglu(leaf)
+    h.backward(dh)
+    ref_in = gu0.float().requires_grad_()
+    a, b = ref_in.chunk(2, dim=-1)
+    ref = F.silu(a) * b
+    ref.backward(dh.float())
+    torch.testing.assert_close(h.float(), ref, rtol=8e-3, atol=1e-5)
+    torch.testing.assert_close(leaf.grad.float(), ref_in.grad, rtol=8e-3, atol=1e-5)
+
+
 def _graph_nodes(fn):
     seen, stack = set(), [fn]
     while stack:

@@ -4,6 +4,7 @@ logsumexp / softmax on the same bf16 logits, and the whole head loss against
 torch's own chunk path (bf16 product, float32 cross-entropy, autograd) and a
 float32 reference."""
 import ctypes
+import math
 
 import pytest
 import torch
@@ -123,7 +124,48 @@ def test_head_loss_scales_by_incoming_gradient_and_ignores_all():
     t_all = torch.full((40,), -100, device=DEV)
     loss0 = head_cross_entropy(x, w, t_all)
     loss0.backward()
-    assert float(loss0) == 0.0 and (x.grad == 0).all() and (w.grad == 0).all()
+    # torch's mean cross-entropy over no counted row is 0 / 0 = NaN; no row
+    # has a gradient
+    ref0 = F.cross_entropy(F.linear(x.detach(), w.detach().to(torch.bfloat16)).float(),
+                           t_all, ignore_index=-100)
+    assert math.isnan(float(loss0)) and math.isnan(float(ref0))
+    assert (x.grad == 0).all() and (w.grad == 0).all()
+
+
+def test_head_loss_without_grad_skips_gradient_products():
+    """Under no_grad, and for inputs that need no gradient, the loss comes from
+    the loss-only pass: the same value as the gradient pass, no autograd node,
+    and no [V, D] fp32 weight-gradient buffer allocated."""
+    torch.manual_seed(5)
+    V, D, N = 5000, 256, 300
+    x = torch.randn(N, D, device=DEV).to(torch.bfloat16)
+    w = (torch.randn(V, D, device=DEV) * D ** -0.5).to(torch.bfloat16)
+    t = torch.randint(0, V, (N,), device=DEV)
+    t[:7] = -100
+    w_req = w.clone().requires_grad_()
+
+    def peak_of(fn):
+        torch.cuda.synchronize()
+        base = torch.cuda.memory_allocated(DEV)
+        torch.cuda.reset_peak_memory_stats(DEV)
+        out = fn()
+        torch.cuda.synchronize()
+        return out, torch.cuda.max_memory_allocated(DEV) - base
+
+    with_grad, peak_grad = peak_of(lambda: head_cross_entropy(x, w_req, t))
+    assert with_grad.grad_fn is not None
+    with_grad = float(with_grad)  # frees the graph and its dx / dW
+    with torch.no_grad():
+        no_grad, peak_nograd = peak_of(lambda: head_cross_entropy(x, w_req, t))
+    plain, peak_plain = peak_of(lambda: head_cross_entropy(x, w, t))  # no input requires grad
+    assert no_grad.grad_fn is None and plain.grad_fn is None
+    assert float(no_grad) == with_grad == float(plain)
+    # the gradient pass also holds the fp32 dW (V * D * 4 bytes, padded) and dx
+    for peak in (peak_nograd, peak_plain):
+        assert peak + 4 * V * D <= peak_grad, (peak, peak_grad)
+    head = LinearCELoss(D, V, weight=torch.nn.Parameter(w.float()))
+    with torch.no_grad():
+        assert head(x[None], t[None]).grad_fn is None
 
 
 def test_module_uses_fused_path_and_matches_cpu_chunks():

@@ -91,3 +91,47 @@ def test_training_module_step():
         losses.append(float(loss))
     assert all(math.isfinite(l) for l in losses)
     assert losses[-1] < losses[0]  # memorising one batch
+
+
+def test_backbone_activation_checkpointing_matches_plain():
+    """TS2TSBackbone(activation_checkpointing=True) (backbone.py:99-102: each
+    layer's forward, attention included, re-runs inside the backward) on a
+    cross_doc_link mask against the same weights without checkpointing: the
+    output bitwise equal, the input and parameter gradients within 2e-2; the
+    attention forward runs twice per layer with checkpointing, once without."""
+    from tagseq2tagseq_amd.modules import TS2TSBackbone
+    T, L = 1024, 4
+    row = synth.config_rows(3, seed=2, T=T)[0]
+    lists = TokenLists(T, [row.spans], DEV, words=row.words, link_rows=[row.link_rows])
+    bm = build_block_mask(*lists.build())
+    assert bm.words > 0
+    torch.manual_seed(4)
+    plain = TS2TSBackbone(L, 256, 4, T, 0.0, 0.0).to(DEV, torch.bfloat16)
+    ckpt = TS2TSBackbone(L, 256, 4, T, 0.0, 0.0, activation_checkpointing=True).to(
+        DEV, torch.bfloat16)
+    ckpt.load_state_dict(plain.state_dict())
+    calls = {"n": 0}
+
+    def count(*_):
+        calls["n"] += 1
+    for m in (plain, ckpt):
+        for layer in m.layers:
+            layer.attn.register_forward_hook(count)
+    x = torch.randn(1, T, 256, device=DEV, dtype=torch.bfloat16)
+    g = torch.randn(1, T, 256, device=DEV, dtype=torch.bfloat16)
+    res = []
+    for m in (plain, ckpt):
+        calls["n"] = 0
+        xi = x.clone().requires_grad_(True)
+        y = m(xi, bm)
+        y.backward(g)
+        res.append((y.detach(), xi.grad, {n: p.grad for n, p in m.named_parameters()},
+                    calls["n"]))
+    (y0, gx0, gp0, n0), (y1, gx1, gp1, n1) = res
+    assert (n0, n1) == (L, 2 * L)
+    assert torch.equal(y0, y1)
+    assert_close(gx1, gx0, 2e-2, 2e-2, "checkpointed input gradient")
+    for name, ref in gp0.items():
+        assert gp1[name] is not None, name
+        scale = float(ref.float().abs().max())
+        assert_close(gp1[name], ref, 2e-2 * max(scale, 1.0), 2e-2, f"checkpointed grad {name}")

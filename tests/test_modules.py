@@ -48,6 +48,20 @@ def test_chunked_loss_matches_full_cross_entropy():
     assert x.grad is not None and torch.isfinite(x.grad).all()
 
 
+def test_chunked_loss_all_ignored_is_nan_like_torch():
+    """Every target ignore_index: torch's mean cross-entropy is 0 / 0 = NaN,
+    and no row has a gradient."""
+    emb = nn.Embedding(20, 8)
+    loss = LinearCELoss(8, 20, weight=emb.weight, chunk=3)
+    x = torch.randn(1, 10, 8, requires_grad=True)
+    t = torch.full((1, 10), -100)
+    got = loss(x, t)
+    ref = F.cross_entropy(x[0] @ emb.weight.T, t[0], ignore_index=-100)
+    assert math.isnan(float(got)) and math.isnan(float(ref))
+    got.backward()
+    assert (x.grad == 0).all()
+
+
 class _Add(nn.Module):
     def __init__(self, c):
         super().__init__()
