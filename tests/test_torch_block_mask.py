@@ -41,26 +41,26 @@ def test_conversion_matches_oracle(name, make):
     assert bm.mask_mod() is not None
 
 
-def _doc_bidirectional(doc):
-    d = torch.from_numpy(doc)
+def _doc_bidirectional(doc, device):
+    d = torch.from_numpy(doc).to(device)
 
     def mod(b, h, q, k):
         return d[q] == d[k]
     return mod
 
 
-def _sliding_window(w):
+def _sliding_window(w, device):
     def mod(b, h, q, k):
         return (q - k).abs() <= w
     return mod
 
 
 NON_CAUSAL = [
-    ("doc bidirectional T384", 384, lambda: _doc_bidirectional(
-        random_row(384, np.random.default_rng(8), max_doc=150)[0])),
-    ("doc bidirectional T1000", 1000, lambda: _doc_bidirectional(
-        row_arrays(synth.config_rows(3, seed=4, T=1000)[0])[0])),
-    ("sliding window 100 T700", 700, lambda: _sliding_window(100)),
+    ("doc bidirectional T384", 384, lambda dev: _doc_bidirectional(
+        random_row(384, np.random.default_rng(8), max_doc=150)[0], dev)),
+    ("doc bidirectional T1000", 1000, lambda dev: _doc_bidirectional(
+        row_arrays(synth.config_rows(3, seed=4, T=1000)[0])[0], dev)),
+    ("sliding window 100 T700", 700, lambda dev: _sliding_window(100, dev)),
 ]
 
 
@@ -109,7 +109,7 @@ def check_any_mask(bm, dense, label):
 
 @pytest.mark.parametrize("name,T,make", NON_CAUSAL, ids=[c[0] for c in NON_CAUSAL])
 def test_conversion_of_non_causal_masks(name, T, make):
-    mod = make()
+    mod = make("cpu")
     bm = from_torch_block_mask(create_block_mask(mod, None, None, T, T, device="cpu"))
     check_any_mask(bm, _dense(mod, T), name)
 
@@ -160,9 +160,8 @@ def test_non_causal_torch_block_mask_against_oracle(name, T, make):
     from tagseq2tagseq_amd.attention import flex_attention
     from tests.helpers import assert_close
     dev = torch.device("cuda:0")
-    mod = make()
-    dense = _dense(mod, T)
-    tbm = create_block_mask(mod, None, None, T, T, device=dev)
+    dense = _dense(make("cpu"), T)
+    tbm = create_block_mask(make(dev), None, None, T, T, device=dev)
     g = torch.Generator().manual_seed(T + 1)
     q, k, v, do = (torch.randn(1, 2, T, 64, generator=g).to(torch.bfloat16).to(dev)
                    for _ in range(4))
