@@ -14,7 +14,10 @@
 //   2. bwd_dkdv:   one work-group per (b, kv head, 128-key tile); walks the
 //                  column's partial and full query tiles (q_num_blocks /
 //                  q_indices, full_q_*) for every query head of the group and
-//                  accumulates dK, dV in registers -- deterministic.
+//                  accumulates dK, dV in registers -- deterministic.  D = 128:
+//                  bwd_dkdv_kernel; D = 64: bwd_dkdv_pair_kernel (two
+//                  work-groups per CU, the work of a key group split between
+//                  two waves).
 //   3. bwd_dq:     one work-group per (b, query head, 128-query tile); walks
 //                  the row's KV tiles and accumulates dQ in registers.
 #include "attn_kernels.h"
@@ -451,6 +454,430 @@ __global__ __launch_bounds__(kDkdvThreads, 1) void bwd_dkdv_kernel(BwdParams p) 
   }
 }
 
+// P of a mixed block in place: P of a masked pair cleared with the pair's
+// sign-extended mask bit (wg: the lane's bitmap word shifted right by its
+// lane group).
+template <int I = 0>
+__device__ __forceinline__ void masked_clear(f32x16& pacc, uint32_t wg) {
+  if constexpr (I < 16) {
+    pacc[I] = __int_as_float(__float_as_int(pacc[I]) & sbfe1_c<acc_tok_bit(I)>(wg));
+    masked_clear<I + 1>(pacc, wg);
+  }
+}
+
+constexpr int kPairWaves = 8;  // 4 key groups x (P / dV wave, dS / dK wave)
+
+// dK, dV at D = 64 for one (b, kv head, 128-key tile), two work-groups per
+// CU, with the work of a key group split between two waves:
+//   P wave:  S = Q K^T, P = exp(S - LSE) (masked pairs cleared), dV^T += dO^T P
+//   dS wave: dP = dO V^T, dS = P (dP - Delta),                dK^T += Q^T dS
+// Each wave holds its key group's K row (P wave) or V row (dS wave) in
+// registers for the whole column and its own accumulator (dV or dK, 32
+// registers), so a key group's dK and dV are complete in one wave each, the
+// end of the kernel has no reduction, and the kernel fits 128 registers and
+// 77.5 KiB of LDS -- two work-groups per CU, whose phases hide each other's
+// copies and barriers (the single-work-group form at D = 64, and this
+// kernel's D = 128 form, which holds one work-group per CU, measure slower
+// than bwd_dkdv_kernel).  Each query tile is consumed as two 64-query
+// halves, both 32-query blocks of a half by each wave; a half is one phase:
+//   P waves:  S, P -> LDS  | dV, then the copies of the half two ahead
+//   dS waves: dP           | P <- LDS, dS, dK
+// with a barrier at the bar (P written to LDS as the bf16 MFMA operand it
+// already is) and one at the end.  The halves of a phase overlap across the
+// two waves of a SIMD (the P wave's exponentials with the dS wave's dP
+// chain, the dS wave's dS with the P wave's dV).  Q, dO, LSE and Delta (in
+// accumulator-row order) and the column bitmap words travel by direct
+// global->LDS copies into three buffers, issued two phases ahead into the
+// buffer freed at the start of the phase, so every copy has a whole phase
+// to land in; the end barrier waits only for the copies older than the
+// phase's own.
+template <int D>
+__global__ __launch_bounds__(kPairWaves * 64) __attribute__((amdgpu_waves_per_eu(4, 4)))
+void bwd_dkdv_pair_kernel(BwdParams p) {
+  static_assert(D == 64, "two work-groups per CU fit at D = 64 only");
+  constexpr int KS = D / 16;
+  constexpr int DT = D / 32;
+  using UC = UnitDma<D, 4>;  // unit copies split over the four P waves
+  constexpr int KP = UC::kPerWave;
+  constexpr int kUnit = UC::kRows * pitch<D>();
+  // Three buffers of each kind: the phase's half, the next one landing, the
+  // one after being issued.  (16-byte aligned: the end of the kernel reuses
+  // the Q and dO units as row buffers, 128 rows over the first two units)
+  __shared__ __align__(16) __bf16 q_s[3 * kUnit], o_s[3 * kUnit];
+  // LSE (log2 domain) and Delta of a half, slot 32 blk + m = query 32 blk +
+  // tok_perm(m) (accumulator-row order); read four at a time.
+  __shared__ __align__(16) float l0[64], l1[64], l2[64], e0[64], e1[64], e2[64];
+  // Column bitmap words of the half's tile: key k's four words (queries
+  // 32 w .. 32 w + 31 of the tile, w = 0..3).
+  __shared__ __align__(16) uint4 m0[kTile], m1[kTile], m2[kTile];
+  // P of each P wave for the dS wave of its key group, [key group][query
+  // block][entry half][lane].
+  __shared__ __align__(16) bf16x8 p_s[4 * 2 * 2 * 64];
+  static_assert(kTile * pitch<D>() <= 2 * kUnit, "the end's row tiles fit two units");
+
+  auto qbuf = [&](auto i) -> __bf16* { return q_s + decltype(i)::value * kUnit; };
+  auto obuf = [&](auto i) -> __bf16* { return o_s + decltype(i)::value * kUnit; };
+  auto lbuf = [&](auto i) -> float* {
+    if constexpr (decltype(i)::value == 0) return l0;
+    else if constexpr (decltype(i)::value == 1) return l1;
+    else return l2;
+  };
+  auto ebuf = [&](auto i) -> float* {
+    if constexpr (decltype(i)::value == 0) return e0;
+    else if constexpr (decltype(i)::value == 1) return e1;
+    else return e2;
+  };
+  auto mbuf = [&](auto i) -> uint4* {
+    if constexpr (decltype(i)::value == 0) return m0;
+    else if constexpr (decltype(i)::value == 1) return m1;
+    else return m2;
+  };
+
+  const int hk = blockIdx.x, b = blockIdx.z;
+  const int tid = threadIdx.x, wave = uniform(tid >> 6), lane = tid & 63;
+  const bool ds_wave = wave >= 4;
+  // Waves w and w + 4 share a SIMD: SIMD s runs the P wave of key group s
+  // and the dS wave of key group 3 - s, so that a SIMD's load is the work of
+  // two key groups from opposite ends of the tile, which evens out tiles
+  // whose allowed pairs sit in some key groups only (document boundaries,
+  // the causal diagonal).
+  const int kw = ds_wave ? 3 - (wave & 3) : (wave & 3);
+  const int g = lane >> 5, n = lane & 31;
+  const int G = p.Hq / p.Hkv;
+  const int mb = p.m.Bm > 1 ? b : 0;
+  const int T = p.T, nt = p.m.nt;
+  const int kt = uniform(p.m.col_order[(size_t)mb * nt + blockIdx.y]);
+  const int k0 = kt * kTile;
+  const int kloc = 32 * kw + n;
+  const float c = p.scale_log2;
+
+  const size_t col = (size_t)mb * nt + kt;
+  const int npart = uniform(p.m.q_num[col]);
+  const int nfull = uniform(p.m.full_q_num[col]);
+  const int nq = npart + nfull;
+  const int nu = G * nq;  // (query head, query tile) items
+  const int32_t* pidx = p.m.q_idx + col * nt;
+  const int32_t* fidx = p.m.full_q_idx + col * nt;
+  const int32_t* pslot = p.m.q_bits_slot + col * nt;
+  const uint32_t* bits_tiles = p.m.tile_bits + kTile * 4;  // column-major halves
+
+  // P wave cw copies instructions cw, cw + 4, ... of the Q and dO units, and
+  // one more each: the Q unit's last (cw 0), the dO unit's last (cw 1), the
+  // LSE row and the bitmap words of keys 0..63 (cw 2), the Delta row and
+  // those of keys 64..127 (cw 3).
+  const int cw = wave & 3;
+  int qoff[KP + 1], ooff[KP + 1];
+#pragma unroll
+  for (int j = 0; j < KP; ++j) {
+    qoff[j] = unit_dma_offset<D>(cw + 4 * j, p.q_st, lane);
+    ooff[j] = unit_dma_offset<D>(cw + 4 * j, p.do_st, lane);
+  }
+  qoff[KP] = unit_dma_offset<D>(UC::kInsts - 1, p.q_st, lane);
+  ooff[KP] = unit_dma_offset<D>(UC::kInsts - 1, p.do_st, lane);
+  const int lrow4 = 4 * (32 * (lane >> 5) + tok_perm(lane & 31));  // LSE / Delta slot `lane`
+
+  // Query-tile list of the column, 64 entries per chunk (lane j: entry
+  // 64 * chunk + j), read back with readlane; reloaded when a chunk changes.
+  int chunk = 0;
+  auto load_chunk = [&](int ch) __attribute__((always_inline)) {
+    const int it = 64 * ch + lane;
+    return make_int2(it < npart ? pidx[it] : (it < nq ? fidx[it - npart] : 0),
+                     it < npart ? pslot[it] : 0);
+  };
+  int2 list_v = load_chunk(0);
+  // (the wait inside the reload keeps the compiler from waiting -- for every
+  // copy in flight -- before each readlane)
+  auto entry = [&](int it) __attribute__((always_inline)) {
+    if ((it >> 6) != chunk) {
+      chunk = it >> 6;
+      list_v = load_chunk(chunk);
+      __builtin_amdgcn_s_waitcnt(0);
+    }
+    return make_int2(__builtin_amdgcn_readlane(list_v.x, it & 63),
+                     __builtin_amdgcn_readlane(list_v.y, it & 63));
+  };
+
+  // The lane's key row of K (P waves) or V (dS waves): the B operand (k = d,
+  // n = key) of S = Q K^T or dP = dO V^T at every k-step, loaded once.  Rows
+  // at or past T read zero.
+  bf16x8 kv[KS];
+  {
+    const __bf16* base = ds_wave ? p.v + b * p.v_sb + hk * p.v_sh : p.k + b * p.k_sb + hk * p.k_sh;
+    const int64_t st = ds_wave ? p.v_st : p.k_st;
+    const auto rs = slice_rsrc(base, st, T, D);
+    const int off = (int)((((int64_t)(k0 + kloc)) * st + 8 * g) * 2);
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+      kv[s] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(rs, off + 32 * s, 0, 0));
+  }
+
+  // Halves h = 0 .. 2 nu - 1: item h / 2, rows 64 (h % 2) of its tile.  The
+  // item of the latest half advanced to:
+  int it_n = 0, hh_n = 0;
+  int2 e_n = make_int2(0, 0);
+  auto advance = [&](int h) __attribute__((always_inline)) {
+    if ((h & 1) == 0 && h > 0 && ++it_n == nq) { it_n = 0; ++hh_n; }
+    if ((h & 1) == 0) e_n = entry(it_n);
+  };
+  struct HalfCopies {
+    u32x4 q, o, l, e, m;  // buffer resources: Q, dO slices, LSE, Delta rows, bitmap
+    int q_ro, o_ro, r4;   // byte offsets of the half's first row
+  };
+  // Copies of the latest half advanced to (rows r0 .. r0 + 63 of head h).
+  auto half_copies = [&](int h_rows) __attribute__((always_inline)) {
+    const int h = hk * G + hh_n;
+    const int r0 = e_n.x * kTile + 64 * (h_rows & 1);
+    const bool partial = it_n < npart;
+    HalfCopies hc;
+    hc.q = slice_words(p.q + b * p.q_sb + h * p.q_sh, p.q_st, T, D);
+    hc.o = slice_words(p.dout + b * p.do_sb + h * p.do_sh, p.do_st, T, D);
+    hc.l = rsrc_words(p.lse2 + ((size_t)b * p.Hq + h) * T, (int64_t)T * 4);
+    hc.e = rsrc_words(p.delta + ((size_t)b * p.Hq + h) * T, (int64_t)T * 4);
+    // full tiles have no bitmap: an empty range (the copies write zeros)
+    hc.m = rsrc_words(bits_tiles + (size_t)(partial ? e_n.y : 0) * kTileBitsWords,
+                      partial ? kTile * 16 : 0);
+    hc.q_ro = uniform(r0 * (int)p.q_st * 2);
+    hc.o_ro = uniform(r0 * (int)p.do_st * 2);
+    hc.r4 = uniform(r0 * 4);
+    return hc;
+  };
+  // A P wave's copies of one half into buffer y: 2 KP + 1 (cw < 2) or
+  // 2 KP + 2 (cw >= 2) loads.
+  auto issue = [&](auto y, const HalfCopies& hc) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < KP; ++j) {
+      lds_copy16(qbuf(y) + (cw + 4 * j) * 64 * 8, qoff[j] + hc.q_ro, hc.q);
+      lds_copy16(obuf(y) + (cw + 4 * j) * 64 * 8, ooff[j] + hc.o_ro, hc.o);
+    }
+    if (cw == 0) {
+      lds_copy16(qbuf(y) + (UC::kInsts - 1) * 64 * 8, qoff[KP] + hc.q_ro, hc.q);
+    } else if (cw == 1) {
+      lds_copy16(obuf(y) + (UC::kInsts - 1) * 64 * 8, ooff[KP] + hc.o_ro, hc.o);
+    } else if (cw == 2) {
+      lds_copy4(lbuf(y), hc.r4 + lrow4, hc.l);
+      lds_copy16(mbuf(y), 16 * lane, hc.m);
+    } else {
+      lds_copy4(ebuf(y), hc.r4 + lrow4, hc.e);
+      lds_copy16(mbuf(y) + 64, 1024 + 16 * lane, hc.m);
+    }
+  };
+  // End of a phase: the P waves keep this phase's copies in flight.
+  auto end_barrier = [&]() __attribute__((always_inline)) {
+    if (ds_wave) vm_barrier<0>();
+    else if (cw < 2) vm_barrier<2 * KP + 1>();
+    else vm_barrier<2 * KP + 2>();
+  };
+  // The bar inside a phase: P written.
+  auto mid_barrier = [&]() __attribute__((always_inline)) {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  };
+
+  // P waves: dV^T; dS waves: dK^T (rows d, lane = key).
+  f32x16 acc[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) acc[dt] = f32x16{};
+
+  // The lane's bitmap words of the half in buffer i (all ones on full tiles).
+  auto words = [&](auto i, bool partial, int h) __attribute__((always_inline)) {
+    uint2 w2 = make_uint2(~0u, ~0u);
+    if (partial) {
+      const uint4 w = mbuf(i)[kloc];
+      w2 = (h & 1) ? make_uint2(w.z, w.w) : make_uint2(w.x, w.y);
+    }
+    return w2;
+  };
+
+  // One phase on the half in buffer x (compile time), copies into buffer y.
+  auto run = [&](auto dsw) __attribute__((always_inline)) {
+    constexpr bool kDs = decltype(dsw)::value;
+    const int nh = 2 * nu;
+    bool pf0 = false, pf1 = false, pf2 = false;  // partial tile of the half in buffer 0 / 1 / 2
+    auto set_pf = [&](auto y, bool v) __attribute__((always_inline)) {
+      if constexpr (decltype(y)::value == 0) pf0 = v;
+      else if constexpr (decltype(y)::value == 1) pf1 = v;
+      else pf2 = v;
+    };
+    auto get_pf = [&](auto x) __attribute__((always_inline)) {
+      if constexpr (decltype(x)::value == 0) return pf0;
+      else if constexpr (decltype(x)::value == 1) return pf1;
+      else return pf2;
+    };
+    auto phase = [&](auto x, auto y, int k) __attribute__((always_inline)) {
+      const uint2 w2 = words(x, get_pf(x), k);
+      const __bf16* qu = qbuf(x);
+      const __bf16* du = obuf(x);
+      if constexpr (!kDs) {
+        // S, P -> LDS
+        const float* lu = lbuf(x);
+        bf16x8 pa[2], pb[2];
+#pragma unroll
+        for (int blk = 0; blk < 2; ++blk) {
+          const uint32_t w = blk ? w2.y : w2.x;
+          if (__ballot(w != 0u) == 0ull) continue;
+          const bool mixed = __ballot(w != ~0u) != 0ull;
+          const int rb = 32 * blk;
+          // every operand of the chain read first (the compiler otherwise
+          // reads each into the same registers right before its MFMA)
+          bf16x8 opd[KS];
+#pragma unroll
+          for (int s = 0; s < KS; ++s) opd[s] = lds_row8<D>(qu, rb + tok_perm(n), 16 * s + 8 * g);
+          f32x16 sacc;
+          __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+          for (int s = 0; s < KS; ++s) sacc = mfma32(opd[s], kv[s], s ? sacc : f32x16{});
+          __builtin_amdgcn_s_setprio(0);
+          const f32x16 lse = acc_rows(lu + rb, g);
+#pragma unroll
+          for (int e = 0; e < 16; ++e) sacc[e] = fast_exp2(fmaf(sacc[e], c, -lse[e]));
+          if (mixed) masked_clear(sacc, w >> g);
+          pa[blk] = pack_half(sacc, 0);
+          pb[blk] = pack_half(sacc, 1);
+          bf16x8* dst = p_s + ((kw * 2 + blk) * 2) * 64 + lane;
+          dst[0] = pa[blk];
+          dst[64] = pb[blk];
+        }
+        mid_barrier();
+        // dV^T += dO^T P
+#pragma unroll
+        for (int blk = 0; blk < 2; ++blk) {
+          const uint32_t w = blk ? w2.y : w2.x;
+          if (__ballot(w != 0u) == 0ull) continue;
+          const int rb = 32 * blk;
+          bf16x8 opd[2 * DT];
+#pragma unroll
+          for (int h2 = 0; h2 < 2; ++h2)
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) opd[h2 * DT + dt] = lds_col8<D>(du, rb + 16 * h2, 32 * dt, lane);
+          __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+          for (int h2 = 0; h2 < 2; ++h2)
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt)
+              acc[dt] = mfma32(opd[h2 * DT + dt], h2 ? pb[blk] : pa[blk], acc[dt]);
+          __builtin_amdgcn_s_setprio(0);
+        }
+        // the copies of half k + 2 (the last half again when there is none:
+        // buffer y is then not read before the kernel ends)
+        const int hl = k + 2 < nh ? k + 2 : nh - 1;
+        if (k + 2 < nh) advance(k + 2);
+        issue(y, half_copies(hl));
+        set_pf(y, it_n < npart);
+      } else {
+        // dP
+        const float* dlu = ebuf(x);
+        f32x16 dp[2];
+#pragma unroll
+        for (int blk = 0; blk < 2; ++blk) {
+          const uint32_t w = blk ? w2.y : w2.x;
+          if (__ballot(w != 0u) == 0ull) continue;
+          const int rb = 32 * blk;
+          bf16x8 opd[KS];
+#pragma unroll
+          for (int s = 0; s < KS; ++s) opd[s] = lds_row8<D>(du, rb + tok_perm(n), 16 * s + 8 * g);
+          __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+          for (int s = 0; s < KS; ++s) dp[blk] = mfma32(opd[s], kv[s], s ? dp[blk] : f32x16{});
+          __builtin_amdgcn_s_setprio(0);
+        }
+        // the item bookkeeping of half k + 2 (the P waves copy it)
+        if (k + 2 < nh) advance(k + 2);
+        set_pf(y, it_n < npart);
+        mid_barrier();
+        // dS = P (dP - Delta), dK^T += Q^T dS
+#pragma unroll
+        for (int blk = 0; blk < 2; ++blk) {
+          const uint32_t w = blk ? w2.y : w2.x;
+          if (__ballot(w != 0u) == 0ull) continue;
+          const int rb = 32 * blk;
+          const f32x16 dl = acc_rows(dlu + rb, g);
+          const bf16x8* src = p_s + ((kw * 2 + blk) * 2) * 64 + lane;
+          const bf16x8 xa = src[0], xb = src[64];
+          f32x16 ds;
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            ds[j] = (dp[blk][j] - dl[j]) * (float)xa[j];
+            ds[8 + j] = (dp[blk][8 + j] - dl[8 + j]) * (float)xb[j];
+          }
+          const bf16x8 sa = pack_half(ds, 0), sb = pack_half(ds, 1);
+          bf16x8 opd[2 * DT];
+#pragma unroll
+          for (int h2 = 0; h2 < 2; ++h2)
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) opd[h2 * DT + dt] = lds_col8<D>(qu, rb + 16 * h2, 32 * dt, lane);
+          __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+          for (int h2 = 0; h2 < 2; ++h2)
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) acc[dt] = mfma32(opd[h2 * DT + dt], h2 ? sb : sa, acc[dt]);
+          __builtin_amdgcn_s_setprio(0);
+        }
+      }
+      end_barrier();
+    };
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    using I2 = std::integral_constant<int, 2>;
+    // Half 0 into buffer 0, then a wait the compiler sees (it also covers
+    // the K / V rows loaded into registers, so no wait for them is left in
+    // the loop) and a barrier; then half 1 into buffer 1.
+    if (nh > 0) {
+      advance(0);
+      if constexpr (!kDs) issue(I0{}, half_copies(0));
+      set_pf(I0{}, it_n < npart);
+    }
+    dma_barrier();
+    if (nh > 0) {
+      const int h1 = nh > 1 ? 1 : 0;
+      if (nh > 1) advance(1);
+      if constexpr (!kDs) issue(I1{}, half_copies(h1));
+      set_pf(I1{}, it_n < npart);
+    }
+    for (int k = 0; k < nh; k += 3) {
+      phase(I0{}, I2{}, k);
+      if (k + 1 >= nh) break;
+      phase(I1{}, I0{}, k + 1);
+      if (k + 2 >= nh) break;
+      phase(I2{}, I1{}, k + 2);
+    }
+  };
+  if (ds_wave) run(std::true_type{});
+  else run(std::false_type{});
+
+  // dK (dS waves, times the scale) and dV (P waves) of the tile as bf16 rows
+  // in LDS (dK over the first two Q units, dV over the first two dO units,
+  // padded pitch), then all eight waves store whole rows, 16 bytes per lane.
+  dma_barrier();
+  {
+    __bf16* rows = ds_wave ? q_s : o_s;
+    const float mul = ds_wave ? p.scale : 1.f;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int a = 0; a < 4; ++a) {
+        bf16x4 w4;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) w4[e] = (__bf16)(acc[dt][4 * a + e] * mul);
+        *reinterpret_cast<bf16x4*>(rows + kloc * pitch<D>() + 32 * dt + acc_row(4 * a, g)) = w4;
+      }
+  }
+  __syncthreads();
+  constexpr int kChunks = D / 8;  // 16-byte pieces per row
+  __bf16* dkp = p.dk + b * p.dk_sb + hk * p.dk_sh;
+  __bf16* dvp = p.dv + b * p.dv_sb + hk * p.dv_sh;
+#pragma unroll
+  for (int j = 0; j < kTile * kChunks / (kPairWaves * 64); ++j) {
+    const int ci = tid + kPairWaves * 64 * j;
+    const int r = ci / kChunks, ch = ci % kChunks;
+    if (k0 + r < T) {
+      const int64_t row = k0 + r;
+      *reinterpret_cast<uint4*>(dkp + row * p.dk_st + 8 * ch) =
+          *reinterpret_cast<const uint4*>(q_s + r * pitch<D>() + 8 * ch);
+      *reinterpret_cast<uint4*>(dvp + row * p.dv_st + 8 * ch) =
+          *reinterpret_cast<const uint4*>(o_s + r * pitch<D>() + 8 * ch);
+    }
+  }
+}
+
 // dQ for one (b, query head, 128-query tile).  Per wave 32 queries; S^T and
 // dP^T put the query in the lane, dS^T feeds dQ^T += K^T dS^T as B operand.
 // The row's KV tiles stream through LDS as 64-key halves (one unit each for
@@ -718,8 +1145,13 @@ hipError_t launch_attn_bwd_phase(int phase, const TensorView& q, const TensorVie
     else hipLaunchKernelGGL(bwd_delta_kernel<128>, grid, dim3(kThreads), 0, stream, p);
   } else if (phase == kBwdDkDv) {
     const dim3 grid(dims.Hkv, nt, dims.B);
+#ifdef T2T_DKDV_CLASSIC
     if (d64) hipLaunchKernelGGL(bwd_dkdv_kernel<64>, grid, dim3(kDkdvThreads), 0, stream, p);
     else hipLaunchKernelGGL(bwd_dkdv_kernel<128>, grid, dim3(kDkdvThreads), 0, stream, p);
+#else
+    if (d64) hipLaunchKernelGGL(bwd_dkdv_pair_kernel<64>, grid, dim3(kPairWaves * 64), 0, stream, p);
+    else hipLaunchKernelGGL(bwd_dkdv_kernel<128>, grid, dim3(kDkdvThreads), 0, stream, p);
+#endif
   } else {  // kBwdDq, kBwdDqDelta
     BwdParams pq = p;
     pq.fuse_delta = phase == kBwdDqDelta;

@@ -113,6 +113,63 @@ __device__ __forceinline__ void unit_dma(__bf16* dst, __amdgpu_buffer_rsrc_t src
       16, mine ? voff[U::kPerWave] + row_off : 0x7ffffff0, 0, 0, 0);
 }
 
+// Raw buffer resource as four scalar words: [base, base + bytes), stride 0,
+// word 3 as slice_rsrc; loads past `bytes` return zeros.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ u32x4 rsrc_words(const void* base, int64_t bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  u32x4 r;
+  r.x = __builtin_amdgcn_readfirstlane((uint32_t)a);
+  r.y = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32) & 0xffffu);
+  r.z = __builtin_amdgcn_readfirstlane((uint32_t)(bytes < 0x7fffffff ? bytes : 0x7fffffff));
+  r.w = 0x00020000u;
+  return r;
+}
+
+// rsrc_words over one [T, D] slice (row stride `st` elements), as slice_rsrc.
+__device__ __forceinline__ u32x4 slice_words(const __bf16* base, int64_t st, int T, int D) {
+  return rsrc_words(base, T > 0 ? ((int64_t)(T - 1) * st + D) * 2 : 0);
+}
+
+// One direct global -> LDS copy (lane l's 16 bytes at byte offset voff into
+// LDS bytes [lds + 16 l, lds + 16 l + 16)) as inline assembly.  The
+// compiler's wait-count pass does not track copies it cannot see, so no LDS
+// read is made to wait for them; a kernel using this form relies on an
+// explicit vmcnt wait before reading what the copies wrote (dma_barrier,
+// vm_barrier).  M0 holds the LDS base; a scalar write of M0 needs one wait
+// state before the copy reads it.  M0 is a reserved register the compiler
+// does not let assembly clobber, and the compiler writes it only for its own
+// LDS copies (__builtin_amdgcn_raw_ptr_buffer_load_lds): a kernel uses
+// either these copies or the builtin ones, never both.
+__device__ __forceinline__ void lds_copy16(const void* lds, int voff, u32x4 rsrc) {
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane(
+      (uint32_t)reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void*)lds));
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               :
+               : "s"(m0), "v"(voff), "s"(rsrc));
+}
+
+// lds_copy16 for 4-byte elements: lane l's dword at byte offset voff into
+// LDS bytes [lds + 4 l, lds + 4 l + 4).
+__device__ __forceinline__ void lds_copy4(const void* lds, int voff, u32x4 rsrc) {
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane(
+      (uint32_t)reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void*)lds));
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dword %1, %2, 0 offen lds"
+               :
+               : "s"(m0), "v"(voff), "s"(rsrc));
+}
+
+// Work-group barrier after this wave's LDS accesses have completed and at
+// most N of its vector-memory loads (the newest ones: loads complete in
+// issue order) are still outstanding -- for pipelines whose copies run more
+// than one barrier ahead.  The compiler does not see the copies issued by
+// lds_copy16 / lds_copy4, so the wait is written here.
+template <int N>
+__device__ __forceinline__ void vm_barrier() {
+  static_assert(N >= 0 && N < 64, "vmcnt is a 6-bit count");
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" : : "n"(N) : "memory");
+}
+
 // Work-group barrier that first drains this wave's outstanding global->LDS
 // copies and LDS accesses (the plain __syncthreads fence would also wait for
 // them, but the explicit form keeps the compiler from hoisting LDS reads
