@@ -111,6 +111,12 @@ def profile_mfma_busy(config: int):
     return {"source": os.path.relpath(path, ROOT), **got} if got else None
 
 
+def dkdv_kernel_name(D: int) -> str:
+    """The dK/dV kernel t2t_attn_bwd runs at head dim D (the pair-split,
+    two-work-groups-per-CU kernel at D = 64)."""
+    return "bwd_dkdv_pair_kernel" if D == 64 else "bwd_dkdv_kernel"
+
+
 def executed_work(bm, B: int, Hq: int, D: int, n_pairs: int, config: int):
     """MFMA work the attention kernels execute for one step, counted from the
     block mask, against the useful work of the metric.
@@ -128,6 +134,7 @@ def executed_work(bm, B: int, Hq: int, D: int, n_pairs: int, config: int):
     the step nothing but these three kernels.  `profile_mfma` repeats the
     per-dispatch MFMA counts of the committed instruction-mix summary, which
     come from the counters (SQ_INSTS_MFMA) of a profiled run of this bench."""
+    dkdv = dkdv_kernel_name(D)
     tc = bm.tile_class
     Bm, nt = tc.shape[0], tc.shape[-1]
     rows_per_mask = B // Bm if Bm < B else 1
@@ -142,9 +149,9 @@ def executed_work(bm, B: int, Hq: int, D: int, n_pairs: int, config: int):
     n_blk = (16 * n_full + int(blocks32.sum())) * rows_per_mask * Hq
     n_fwd = (8 * n_full + int(units_fwd.sum())) * rows_per_mask * Hq
     mf = {"attn_fwd_bf16_kernel": n_fwd * D // 4,
-          "bwd_dkdv_kernel": n_blk * D // 4,
+          dkdv: n_blk * D // 4,
           "bwd_dq_kernel": n_blk * 3 * D // 16}
-    useful = {"attn_fwd_bf16_kernel": 4.0, "bwd_dkdv_kernel": 8.0, "bwd_dq_kernel": 6.0}
+    useful = {"attn_fwd_bf16_kernel": 4.0, dkdv: 8.0, "bwd_dq_kernel": 6.0}
     out = {}
     executed = 0.0
     for k, n in mf.items():
@@ -944,7 +951,7 @@ def main():
     base = D * n_pairs * Hq
     kernels = {
         "attn_fwd_bf16_kernel": (t_fwd, 4.0 * base),
-        "bwd_dkdv_kernel": (t_dkdv, 8.0 * base),
+        dkdv_kernel_name(D): (t_dkdv, 8.0 * base),
         "bwd_dq_kernel": (t_dq, 6.0 * base),
     }
     dom = max(kernels, key=lambda n: kernels[n][0])
@@ -1012,7 +1019,7 @@ def main():
             "mask_meta (3 launches)": round(t_meta, 4),
             "attn_fwd_bf16_kernel": round(t_fwd, 4),
             "bwd_delta_kernel": round(t_pre, 4),
-            "bwd_dkdv_kernel": round(t_dkdv, 4),
+            dkdv_kernel_name(D): round(t_dkdv, 4),
             "bwd_dq_kernel": round(t_dq, 4),
         },
         # The step's backward is t2t_attn_bwd: dQ computing Delta itself, then

@@ -49,7 +49,7 @@ from .modules import Layer
 
 PEAK_BF16_TFLOPS = 2516.6
 SIMDS, CLOCK_HZ = 1024, 2.4e9
-ATTN_KERNELS = ("attn_fwd_bf16_kernel", "bwd_dq_kernel", "bwd_dkdv_kernel")
+ATTN_KERNELS = ("attn_fwd_bf16_kernel", "bwd_dq_kernel", "bwd_dkdv_kernel", "bwd_dkdv_pair_kernel")
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 PROFILE = os.path.join(ROOT, "profiles", "layer_mfma.txt")
 PASS_CALLS = 3  # layer fwd+bwd calls per point in the counter pass

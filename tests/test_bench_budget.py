@@ -25,7 +25,7 @@ def test_executed_work_counts_nonempty_blocks(T, words, D, Hq):
     units = pad.reshape(nt * 4, 32, nt * 2, 64).any((1, 3)).sum()    # 32 queries x 64 keys
     ew = bench.executed_work(bm, 1, Hq, D, n_pairs, config=0)
     assert ew["attn_fwd_bf16_kernel"]["mfma_per_launch"] == units * Hq * D // 4
-    assert ew["bwd_dkdv_kernel"]["mfma_per_launch"] == blk * Hq * D // 4
+    assert ew[bench.dkdv_kernel_name(D)]["mfma_per_launch"] == blk * Hq * D // 4
     assert ew["bwd_dq_kernel"]["mfma_per_launch"] == blk * Hq * 3 * D // 16
     step = ew["step"]
     useful = 14 * D * n_pairs * Hq
