@@ -611,12 +611,28 @@ void bwd_dkdv_pair_kernel(BwdParams p) {
       kv[s] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(rs, off + 32 * s, 0, 0));
   }
 
+  // Buffer resources of the current query head's Q and dO slices and LSE
+  // and Delta rows, rebuilt only when the walk moves to the next head.
+  int hh_n = 0;
+  u32x4 rq, ro, rl, re;
+  auto head_rsrc = [&]() __attribute__((always_inline)) {
+    const int h = hk * G + hh_n;
+    rq = slice_words(p.q + b * p.q_sb + h * p.q_sh, p.q_st, T, D);
+    ro = slice_words(p.dout + b * p.do_sb + h * p.do_sh, p.do_st, T, D);
+    rl = rsrc_words(p.lse2 + ((size_t)b * p.Hq + h) * T, (int64_t)T * 4);
+    re = rsrc_words(p.delta + ((size_t)b * p.Hq + h) * T, (int64_t)T * 4);
+  };
+  head_rsrc();
   // Halves h = 0 .. 2 nu - 1: item h / 2, rows 64 (h % 2) of its tile.  The
   // item of the latest half advanced to:
-  int it_n = 0, hh_n = 0;
+  int it_n = 0;
   int2 e_n = make_int2(0, 0);
   auto advance = [&](int h) __attribute__((always_inline)) {
-    if ((h & 1) == 0 && h > 0 && ++it_n == nq) { it_n = 0; ++hh_n; }
+    if ((h & 1) == 0 && h > 0 && ++it_n == nq) {
+      it_n = 0;
+      ++hh_n;
+      head_rsrc();
+    }
     if ((h & 1) == 0) e_n = entry(it_n);
   };
   struct HalfCopies {
@@ -625,14 +641,13 @@ void bwd_dkdv_pair_kernel(BwdParams p) {
   };
   // Copies of the latest half advanced to (rows r0 .. r0 + 63 of head h).
   auto half_copies = [&](int h_rows) __attribute__((always_inline)) {
-    const int h = hk * G + hh_n;
     const int r0 = e_n.x * kTile + 64 * (h_rows & 1);
     const bool partial = it_n < npart;
     HalfCopies hc;
-    hc.q = slice_words(p.q + b * p.q_sb + h * p.q_sh, p.q_st, T, D);
-    hc.o = slice_words(p.dout + b * p.do_sb + h * p.do_sh, p.do_st, T, D);
-    hc.l = rsrc_words(p.lse2 + ((size_t)b * p.Hq + h) * T, (int64_t)T * 4);
-    hc.e = rsrc_words(p.delta + ((size_t)b * p.Hq + h) * T, (int64_t)T * 4);
+    hc.q = rq;
+    hc.o = ro;
+    hc.l = rl;
+    hc.e = re;
     // full tiles have no bitmap: an empty range (the copies write zeros)
     hc.m = rsrc_words(bits_tiles + (size_t)(partial ? e_n.y : 0) * kTileBitsWords,
                       partial ? kTile * 16 : 0);
@@ -643,22 +658,26 @@ void bwd_dkdv_pair_kernel(BwdParams p) {
   };
   // A P wave's copies of one half into buffer y: 2 KP + 1 (cw < 2) or
   // 2 KP + 2 (cw >= 2) loads.
+  // (LDS addresses as integers: constants plus the wave's offset)
+  const uint32_t q_u = lds_u32(q_s), o_u = lds_u32(o_s), cw_u = (uint32_t)cw * 1024u;
   auto issue = [&](auto y, const HalfCopies& hc) __attribute__((always_inline)) {
+    constexpr uint32_t yo = decltype(y)::value * kUnit * 2;  // bytes
 #pragma unroll
     for (int j = 0; j < KP; ++j) {
-      lds_copy16(qbuf(y) + (cw + 4 * j) * 64 * 8, qoff[j] + hc.q_ro, hc.q);
-      lds_copy16(obuf(y) + (cw + 4 * j) * 64 * 8, ooff[j] + hc.o_ro, hc.o);
+      lds_copy16_m0(uniform(q_u + yo + cw_u + 4096u * j), qoff[j] + hc.q_ro, hc.q);
+      lds_copy16_m0(uniform(o_u + yo + cw_u + 4096u * j), ooff[j] + hc.o_ro, hc.o);
     }
+    constexpr uint32_t last = (UC::kInsts - 1) * 1024u;
     if (cw == 0) {
-      lds_copy16(qbuf(y) + (UC::kInsts - 1) * 64 * 8, qoff[KP] + hc.q_ro, hc.q);
+      lds_copy16_m0(q_u + yo + last, qoff[KP] + hc.q_ro, hc.q);
     } else if (cw == 1) {
-      lds_copy16(obuf(y) + (UC::kInsts - 1) * 64 * 8, ooff[KP] + hc.o_ro, hc.o);
+      lds_copy16_m0(o_u + yo + last, ooff[KP] + hc.o_ro, hc.o);
     } else if (cw == 2) {
-      lds_copy4(lbuf(y), hc.r4 + lrow4, hc.l);
-      lds_copy16(mbuf(y), 16 * lane, hc.m);
+      lds_copy4_m0(lds_u32(lbuf(y)), hc.r4 + lrow4, hc.l);
+      lds_copy16_m0(lds_u32(mbuf(y)), 16 * lane, hc.m);
     } else {
-      lds_copy4(ebuf(y), hc.r4 + lrow4, hc.e);
-      lds_copy16(mbuf(y) + 64, 1024 + 16 * lane, hc.m);
+      lds_copy4_m0(lds_u32(ebuf(y)), hc.r4 + lrow4, hc.e);
+      lds_copy16_m0(lds_u32(mbuf(y)) + 1024u, 1024 + 16 * lane, hc.m);
     }
   };
   // End of a phase: the P waves keep this phase's copies in flight.

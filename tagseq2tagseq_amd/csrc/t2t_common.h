@@ -149,6 +149,25 @@ __device__ __forceinline__ void lds_copy16(const void* lds, int voff, u32x4 rsrc
                : "s"(m0), "v"(voff), "s"(rsrc));
 }
 
+// lds_copy16 / lds_copy4 with the LDS byte address given as a wave-uniform
+// integer (e.g. a __shared__ array's lds_u32 plus a constant offset), which
+// keeps pointer conversions off the issuing path.
+__device__ __forceinline__ void lds_copy16_m0(uint32_t m0, int voff, u32x4 rsrc) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               :
+               : "s"(m0), "v"(voff), "s"(rsrc));
+}
+__device__ __forceinline__ void lds_copy4_m0(uint32_t m0, int voff, u32x4 rsrc) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dword %1, %2, 0 offen lds"
+               :
+               : "s"(m0), "v"(voff), "s"(rsrc));
+}
+
+// LDS byte address of a __shared__ object (a constant for a named array).
+__device__ __forceinline__ uint32_t lds_u32(const void* x) {
+  return (uint32_t)reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void*)x);
+}
+
 // lds_copy16 for 4-byte elements: lane l's dword at byte offset voff into
 // LDS bytes [lds + 4 l, lds + 4 l + 4).
 __device__ __forceinline__ void lds_copy4(const void* lds, int voff, u32x4 rsrc) {
