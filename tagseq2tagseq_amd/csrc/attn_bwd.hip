@@ -140,7 +140,6 @@ __global__ __launch_bounds__(kDkdvThreads, 1) void bwd_dkdv_kernel(BwdParams p) 
   // 32 blk + tok_perm(m) (accumulator-row order).
   // (16-byte aligned: rows are read four at a time)
   __shared__ __align__(16) float lse_lo[64], lse_hi[64], dl_lo[64], dl_hi[64];
-  __shared__ uint4 dma_scratch[64];
 
   const int hk = blockIdx.x, b = blockIdx.z;
   const int tid = threadIdx.x, wave = uniform(tid >> 6), lane = tid & 63;
@@ -204,10 +203,10 @@ __global__ __launch_bounds__(kDkdvThreads, 1) void bwd_dkdv_kernel(BwdParams p) 
     const auto krs = slice_rsrc(p.k + b * p.k_sb + hk * p.k_sh, p.k_st, T, D);
     const auto vrs = slice_rsrc(p.v + b * p.v_sb + hk * p.v_sh, p.v_st, T, D);
     const int kr2 = (int)p.k_st * 2, vr2 = (int)p.v_st * 2;
-    unit_dma<D, kDkdvWaves>(k_s, krs, koff, k0 * kr2, wave, 4, dma_scratch);
-    unit_dma<D, kDkdvWaves>(k_s + kUnit, krs, koff, (k0 + 64) * kr2, wave, 5, dma_scratch);
-    unit_dma<D, kDkdvWaves>(v_s, vrs, voff, k0 * vr2, wave, 6, dma_scratch);
-    unit_dma<D, kDkdvWaves>(v_s + kUnit, vrs, voff, (k0 + 64) * vr2, wave, 7, dma_scratch);
+    unit_dma<D, kDkdvWaves>(k_s, krs, koff, k0 * kr2, wave, 4);
+    unit_dma<D, kDkdvWaves>(k_s + kUnit, krs, koff, (k0 + 64) * kr2, wave, 5);
+    unit_dma<D, kDkdvWaves>(v_s, vrs, voff, k0 * vr2, wave, 6);
+    unit_dma<D, kDkdvWaves>(v_s + kUnit, vrs, voff, (k0 + 64) * vr2, wave, 7);
   }
   auto entry = [&](int it) {
     if ((it >> 6) != chunk) {
@@ -230,7 +229,7 @@ __global__ __launch_bounds__(kDkdvThreads, 1) void bwd_dkdv_kernel(BwdParams p) 
   const float inv_c = 1.f / c;
   auto load_q_part = [&](__bf16* qd, float* ld, int h, int r0) {
     const auto qrs = slice_rsrc(p.q + b * p.q_sb + h * p.q_sh, p.q_st, T, D);
-    unit_dma<D, kDkdvWaves>(qd, qrs, qoff, r0 * (int)p.q_st * 2, wave, 0, dma_scratch);
+    unit_dma<D, kDkdvWaves>(qd, qrs, qoff, r0 * (int)p.q_st * 2, wave, 0);
     const auto lrs = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<float*>(p.lse2 + ((size_t)b * p.Hq + h) * T), 0, T * 4, 0x00020000);
     if (wave == 2) {
@@ -240,7 +239,7 @@ __global__ __launch_bounds__(kDkdvThreads, 1) void bwd_dkdv_kernel(BwdParams p) 
   };
   auto load_do_part = [&](__bf16* dd, float* dld, int h, int r0) {
     const auto drs = slice_rsrc(p.dout + b * p.do_sb + h * p.do_sh, p.do_st, T, D);
-    unit_dma<D, kDkdvWaves>(dd, drs, ooff, r0 * (int)p.do_st * 2, wave, 1, dma_scratch);
+    unit_dma<D, kDkdvWaves>(dd, drs, ooff, r0 * (int)p.do_st * 2, wave, 1);
     const auto drs2 = __builtin_amdgcn_make_buffer_rsrc(p.delta + ((size_t)b * p.Hq + h) * T, 0,
                                                         T * 4, 0x00020000);
     if (wave == 3) {
@@ -914,7 +913,6 @@ __global__ __launch_bounds__(kThreads, 2) void bwd_dq_kernel(BwdParams p) {
   constexpr int kUnit = U::kRows * pitch<D>();
   __shared__ __bf16 k_lo[kUnit], k_hi[kUnit], v_lo[kUnit], v_hi[kUnit];
   __shared__ uint32_t bits_lds[2][kTile * 4];
-  __shared__ uint4 dma_scratch[64];  // sink of the copies no wave owns
 
   const int b = blockIdx.z;
   const int tid = threadIdx.x, wave = uniform(tid >> 6), lane = tid & 63;
@@ -992,8 +990,8 @@ __global__ __launch_bounds__(kThreads, 2) void bwd_dq_kernel(BwdParams p) {
   const int k_row2 = (int)p.k_st * 2, v_row2 = (int)p.v_st * 2;
   // K and V rows [t0, t0 + 64) into one half's units (rows past T read zero).
   auto load_half = [&](__bf16* kd, __bf16* vd, int t0) {
-    unit_dma<D>(kd, krs, koff, t0 * k_row2, wave, 0, dma_scratch);
-    unit_dma<D>(vd, vrs, voff, t0 * v_row2, wave, 1, dma_scratch);
+    unit_dma<D>(kd, krs, koff, t0 * k_row2, wave, 0);
+    unit_dma<D>(vd, vrs, voff, t0 * v_row2, wave, 1);
   };
   // Row-major half (128 queries x 4 words) of the bitmap of iteration it
   // (KV tile kt, slot kv_bits_off + kt); waves w and w + 2 copy the same KiB.

@@ -56,7 +56,6 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(FwdParams p)
   constexpr int kUnit = U::kRows * pitch<D>();
   __shared__ __bf16 k_lo[kUnit], k_hi[kUnit], v_lo[kUnit], v_hi[kUnit];
   __shared__ uint32_t bits_lds[2][kTile * 4];
-  __shared__ uint4 dma_scratch[64];  // sink of the copies no wave owns
 
   const int b = blockIdx.z;
   const int tid = threadIdx.x, wave = uniform(tid >> 6), lane = tid & 63;
@@ -117,8 +116,8 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(FwdParams p)
   const auto vrs = slice_rsrc(vbase, p.v_st, T, D);
   const int k_row2 = (int)p.k_st * 2, v_row2 = (int)p.v_st * 2;
   auto load_half = [&](__bf16* kd, __bf16* vd, int t0) {
-    unit_dma<D>(kd, krs, koff, t0 * k_row2, wave, 0, dma_scratch);
-    unit_dma<D>(vd, vrs, voff, t0 * v_row2, wave, 1, dma_scratch);
+    unit_dma<D>(kd, krs, koff, t0 * k_row2, wave, 0);
+    unit_dma<D>(vd, vrs, voff, t0 * v_row2, wave, 1);
   };
   // Row-major half (128 queries x 4 words) of the bitmap of iteration it
   // (KV tile kt, slot kv_bits_off + kt); each wave copies 1 KiB (waves w and

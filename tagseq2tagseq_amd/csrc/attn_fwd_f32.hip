@@ -67,7 +67,6 @@ __global__ __launch_bounds__(kThreads, 1) void attn_fwd_f32_kernel(FwdF32Params 
   static_assert(U::kRows * pitch<2 * D>() == 2 * kUnit, "fp32 unit = bf16 unit of 2 D");
   __shared__ __attribute__((aligned(16))) float k_lo[kUnit], k_hi[kUnit], v_lo[kUnit], v_hi[kUnit];
   __shared__ __attribute__((aligned(16))) uint32_t bits_lds[2][kTile * 4];
-  __shared__ uint4 dma_scratch[64];
 
   const int h = blockIdx.x, b = blockIdx.z;
   const int tid = threadIdx.x, wave = uniform(tid >> 6), lane = tid & 63;
@@ -124,8 +123,8 @@ __global__ __launch_bounds__(kThreads, 1) void attn_fwd_f32_kernel(FwdF32Params 
   const int k_row4 = (int)p.k_st * 4, v_row4 = (int)p.v_st * 4;
   // K and V rows [t0, t0 + 64) into one half's units (rows past T read zero).
   auto load_half = [&](float* kd, float* vd, int t0) {
-    unit_dma<2 * D>(reinterpret_cast<__bf16*>(kd), krs, koff, t0 * k_row4, wave, 0, dma_scratch);
-    unit_dma<2 * D>(reinterpret_cast<__bf16*>(vd), vrs, voff, t0 * v_row4, wave, 1, dma_scratch);
+    unit_dma<2 * D>(reinterpret_cast<__bf16*>(kd), krs, koff, t0 * k_row4, wave, 0);
+    unit_dma<2 * D>(reinterpret_cast<__bf16*>(vd), vrs, voff, t0 * v_row4, wave, 1);
   };
   // bitmap of iteration it: KV tile kt, slot kv_bits_off + kt
   auto load_bits = [&](int it, int kt) {

@@ -89,28 +89,26 @@ __device__ __forceinline__ int unit_dma_offset(int i, int64_t st, int lane) {
 }
 
 // Wave `wave`'s share of a unit copy by NW waves: instructions wave + NW j,
-// plus the unit's last instruction, which every wave issues so that the
-// sequence has no branch: wave `extra_wave` copies it into the unit, the
-// other waves send an out-of-range load (zeros, no memory touched) into
-// `scratch` (1 KiB of LDS nobody reads).  voff[j] = unit_dma_offset(wave +
-// NW j), voff[kPerWave] = unit_dma_offset(kInsts - 1).
+// and the unit's last instruction in wave `extra_wave` only (a wave-uniform
+// branch; the other waves issue nothing for it).  voff[j] =
+// unit_dma_offset(wave + NW j), voff[kPerWave] = unit_dma_offset(kInsts - 1).
 // `src` covers the whole [T, D] slice (slice_rsrc) and `row_off` is the byte
 // offset of the unit's first row; it is added to the per-lane offset, whose
 // range check then zero-fills rows at or past T (the host keeps every such
 // offset below 2^31).
 template <int D, int NW = kWaves>
 __device__ __forceinline__ void unit_dma(__bf16* dst, __amdgpu_buffer_rsrc_t src, const int* voff,
-                                         int row_off, int wave, int extra_wave, void* scratch) {
+                                         int row_off, int wave, int extra_wave) {
   using U = UnitDma<D, NW>;
 #pragma unroll
   for (int j = 0; j < U::kPerWave; ++j)
     __builtin_amdgcn_raw_ptr_buffer_load_lds(
         src, (__attribute__((address_space(3))) void*)(dst + (wave + NW * j) * 64 * 8), 16,
         voff[j] + row_off, 0, 0, 0);
-  const bool mine = wave == extra_wave;
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(
-      src, (__attribute__((address_space(3))) void*)(mine ? (void*)(dst + (U::kInsts - 1) * 64 * 8) : scratch),
-      16, mine ? voff[U::kPerWave] + row_off : 0x7ffffff0, 0, 0, 0);
+  if (wave == extra_wave)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        src, (__attribute__((address_space(3))) void*)(dst + (U::kInsts - 1) * 64 * 8), 16,
+        voff[U::kPerWave] + row_off, 0, 0, 0);
 }
 
 // Raw buffer resource as four scalar words: [base, base + bytes), stride 0,
