@@ -994,16 +994,17 @@ __global__ __launch_bounds__(kThreads, 2) void bwd_dq_kernel(BwdParams p) {
     unit_dma<D>(vd, vrs, voff, t0 * v_row2, wave, 1);
   };
   // Row-major half (128 queries x 4 words) of the bitmap of iteration it
-  // (KV tile kt, slot kv_bits_off + kt); waves w and w + 2 copy the same KiB.
+  // (KV tile kt, slot kv_bits_off + kt); waves 0 and 1 copy 1 KiB each.
   // Tiles without a bitmap copy zeros.
   auto load_bits = [&](int it, int kt) {
     const bool has = it < npart;
     const auto rs = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint32_t*>(bits_row + (has ? (size_t)kt * kTileBitsWords : 0)), 0,
         has ? kTile * 16 : 0, 0x00020000);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(
-        rs, (__attribute__((address_space(3))) void*)(&bits_lds[it & 1][(wave & 1) * 256]), 16,
-        (wave & 1) * 1024 + lane * 16, 0, 0, 0);
+    if (wave < 2)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rs, (__attribute__((address_space(3))) void*)(&bits_lds[it & 1][wave * 256]), 16,
+          wave * 1024 + lane * 16, 0, 0, 0);
   };
 
   f32x16 dqacc[DT];
