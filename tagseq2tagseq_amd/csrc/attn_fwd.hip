@@ -23,8 +23,9 @@
 // Pipeline: each KV tile is consumed as two 64-key halves (K rows + V rows,
 // one LDS unit each).  While a wave computes on one half, the other half's
 // units are being filled by direct global->LDS copies issued right after the
-// barrier that retired them, together with the next tile's bitmap; one
-// barrier per half.  No staging registers and no register->LDS stores.
+// barrier that retired them; each lane loads its query row's words of the
+// next tile's bitmap into registers at the same point.  One barrier per half.
+// No staging registers and no register->LDS stores.
 //
 // Work-groups are dispatched longest row first (row_order); with grouped-query
 // heads the heads of one KV head and row run back to back on one XCD
@@ -55,7 +56,6 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(FwdParams p)
   using U = UnitDma<D>;
   constexpr int kUnit = U::kRows * pitch<D>();
   __shared__ __bf16 k_lo[kUnit], k_hi[kUnit], v_lo[kUnit], v_hi[kUnit];
-  __shared__ uint32_t bits_lds[2][kTile * 4];
 
   const int b = blockIdx.z;
   const int tid = threadIdx.x, wave = uniform(tid >> 6), lane = tid & 63;
@@ -119,18 +119,15 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(FwdParams p)
     unit_dma<D>(kd, krs, koff, t0 * k_row2, wave, 0);
     unit_dma<D>(vd, vrs, voff, t0 * v_row2, wave, 1);
   };
-  // Row-major half (128 queries x 4 words) of the bitmap of iteration it
-  // (KV tile kt, slot kv_bits_off + kt): waves 0 and 1 copy 1 KiB each.
-  // (Tiles without a bitmap, it >= npart, copy zeros.)
+  // The lane's four bitmap words (its query row of the tile's row-major
+  // bitmap) of iteration it, loaded into registers one tile ahead.  (Tiles
+  // without a bitmap, it >= npart, read zeros.)
   auto load_bits = [&](int it, int kt) {
     const bool has = it < npart;
     const auto rs = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint32_t*>(bits_row + (has ? (size_t)kt * kTileBitsWords : 0)), 0,
         has ? kTile * 16 : 0, 0x00020000);
-    if (wave < 2)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          rs, (__attribute__((address_space(3))) void*)(&bits_lds[it & 1][wave * 256]), 16,
-          wave * 1024 + lane * 16, 0, 0, 0);
+    return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, qloc * 16, 0, 0));
   };
 
   f32x16 oacc[DT];
@@ -250,9 +247,10 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(FwdParams p)
   };
 
   int k0_next = ntiles > 0 ? tile_of(0) * kTile : 0;
+  uint4 mb_next = make_uint4(~0u, ~0u, ~0u, ~0u);
   if (ntiles > 0) {
+    if (npart > 0) mb_next = load_bits(0, k0_next / kTile);
     load_half(k_lo, v_lo, k0_next);
-    if (npart > 0) load_bits(0, k0_next / kTile);
   }
   for (int it = 0; it < ntiles; ++it) {
     const bool partial = it < npart;
@@ -260,8 +258,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(FwdParams p)
     // Keys [k0, k0 + 64): its units and bitmap have landed; the other half's
     // units are free again.
     dma_barrier();
-    uint4 mbits = make_uint4(~0u, ~0u, ~0u, ~0u);
-    if (partial) mbits = *reinterpret_cast<const uint4*>(&bits_lds[it & 1][qloc * 4]);
+    const uint4 mbits = partial ? mb_next : make_uint4(~0u, ~0u, ~0u, ~0u);
     load_half(k_hi, v_hi, k0 + 64);
     half_step(k_lo, v_lo, mbits.x, mbits.y, partial);
 
@@ -273,8 +270,8 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(FwdParams p)
       k0_next = tile_of(it + 1) * kTile;
     }
     if (more) {
+      if (it + 1 < npart) mb_next = load_bits(it + 1, k0_next / kTile);
       load_half(k_lo, v_lo, k0_next);
-      load_bits(it + 1, k0_next / kTile);
     }
     half_step(k_hi, v_hi, mbits.z, mbits.w, partial);
   }
