@@ -96,6 +96,19 @@ def test_gqa_grouped_dispatch(gpu_device):
     _oracle_check(rows, 2, 8, 2, 512, 128, seed=21, device=gpu_device)
 
 
+@pytest.mark.parametrize("B,Hq,Hkv,T,D", [
+    (2, 6, 2, 512, 64),    # G = 3, Hkv * tiles = 8: grouped placement, rounds of 24 slots
+    (1, 8, 1, 1024, 128),  # G = 8, Hkv * tiles = 8: grouped placement, rounds of 64 slots
+    (1, 6, 2, 384, 128),   # G = 3, Hkv * tiles = 6: heads fastest
+])
+def test_gqa_group_sizes(B, Hq, Hkv, T, D, gpu_device):
+    """Group sizes other than 2 and 4 on both of head_and_slot's paths:
+    every (query head, tile) work-group must land on a distinct slot."""
+    rng = np.random.default_rng(Hq * 100 + T)
+    rows = [random_row(T, rng, words=2, uncovered=True, max_doc=300) for _ in range(B)]
+    _oracle_check(rows, B, Hq, Hkv, T, D, seed=Hq + T, device=gpu_device)
+
+
 @pytest.mark.parametrize("scale", [0.02, 0.5])
 def test_explicit_scale(scale, gpu_device):
     """A non-default scale reaches the forward's score scaling and the
