@@ -117,14 +117,21 @@ def dkdv_kernel_name(D: int) -> str:
     return "bwd_dkdv_pair_kernel" if D == 64 else "bwd_dkdv_kernel"
 
 
+def fwd_step_keys(D: int) -> int:
+    """Keys per step of the bf16 forward kernel at head dim D (64-key halves
+    at D = 64, 32-key quarters at D = 128; launch_attn_fwd_bf16)."""
+    return 64 if D == 64 else 32
+
+
 def executed_work(bm, B: int, Hq: int, D: int, n_pairs: int, config: int):
     """MFMA work the attention kernels execute for one step, counted from the
     block mask, against the useful work of the metric.
 
-    The kernels compute whole MFMA blocks: the forward a 32-query x 64-key
-    unit of a non-skip tile when any pair in it is allowed (D / 4 MFMAs: the
-    scores and P V), dK/dV and dQ a 32 x 32 block when any pair in it is
-    allowed (D / 4 MFMAs: S, dP, dV, dK; 3 D / 16: S, dP, dQ).  An MFMA
+    The kernels compute whole MFMA blocks: the forward a 32-query x SK-key
+    step of a non-skip tile (SK = fwd_step_keys(D)) when any pair in it is
+    allowed (SK D / 128 MFMAs: the scores and P V), dK/dV and dQ a 32 x 32
+    block when any pair in it is allowed (D / 4 MFMAs: S, dP, dV, dK;
+    3 D / 16: S, dP, dQ).  An MFMA
     (32 x 32 x 16) is 32768 FLOP.  Useful work is 4 D (forward), 8 D (dK/dV,
     which recomputes S and dP) and 6 D (dQ, the same recompute) FLOP per
     allowed pair, and 14 D per pair for the step (the metric's convention,
@@ -145,10 +152,11 @@ def executed_work(bm, B: int, Hq: int, D: int, n_pairs: int, config: int):
     words = bm.tile_bits[slots, 0] != 0 if slots.numel() else torch.zeros(
         (0, 128, 4), dtype=torch.bool, device=tc.device)
     blocks32 = words.view(-1, 4, 32, 4).any(2)                        # [P, q blk, k blk]
-    units_fwd = words.view(-1, 4, 32, 2, 2).any(4).any(2)             # [P, q blk, k half]
+    sk = fwd_step_keys(D)
+    units_fwd = words.view(-1, 4, 32, 128 // sk, sk // 32).any(4).any(2)  # [P, q blk, k step]
     n_blk = (16 * n_full + int(blocks32.sum())) * rows_per_mask * Hq
-    n_fwd = (8 * n_full + int(units_fwd.sum())) * rows_per_mask * Hq
-    mf = {"attn_fwd_bf16_kernel": n_fwd * D // 4,
+    n_fwd = (4 * (128 // sk) * n_full + int(units_fwd.sum())) * rows_per_mask * Hq
+    mf = {"attn_fwd_bf16_kernel": n_fwd * sk * D // 128,
           dkdv: n_blk * D // 4,
           "bwd_dq_kernel": n_blk * 3 * D // 16}
     useful = {"attn_fwd_bf16_kernel": 4.0, dkdv: 8.0, "bwd_dq_kernel": 6.0}
@@ -164,7 +172,7 @@ def executed_work(bm, B: int, Hq: int, D: int, n_pairs: int, config: int):
                    "useful_gflop": round(step_useful / 1e9, 2),
                    "executed_over_useful": round(executed / step_useful, 4),
                    "busy_needed_for_50pct": round(0.5 * executed / step_useful, 4),
-                   "allowed_share_fwd_units": round(n_pairs * Hq / (2048.0 * n_fwd), 4),
+                   "allowed_share_fwd_units": round(n_pairs * Hq / (32.0 * sk * n_fwd), 4),
                    "allowed_share_bwd_blocks": round(n_pairs * Hq / (1024.0 * n_blk), 4)}
     from tagseq2tagseq_amd.rocprof_summary import read_mfma_counts
     path = os.path.join(ROOT, "profiles", f"instruction_mix_config{config}.txt")

@@ -20,12 +20,15 @@
 // probabilities stay below 256, far inside fp32 / bf16 range, and O is
 // rescaled a handful of times per row instead of at every block.
 //
-// Pipeline: each KV tile is consumed as two 64-key halves (K rows + V rows,
-// one LDS unit each).  While a wave computes on one half, the other half's
-// units are being filled by direct global->LDS copies issued right after the
-// barrier that retired them; each lane loads its query row's words of the
-// next tile's bitmap into registers at the same point.  One barrier per half.
-// No staging registers and no register->LDS stores.
+// Pipeline: each KV tile is consumed in steps of SK keys (K rows + V rows,
+// one LDS unit each): two 64-key halves at D = 64, four 32-key quarters at
+// D = 128, where the smaller step's registers and LDS units let three
+// work-groups share a CU instead of two.  While a wave computes on one
+// step, the other buffer's units are being filled by direct global->LDS
+// copies issued right after the barrier that retired them; each lane loads
+// its query row's words of the next tile's bitmap into registers at the
+// tile's last step.  One barrier per step.  No staging registers and no
+// register->LDS stores.
 //
 // Work-groups are dispatched longest row first (row_order); with grouped-query
 // heads the heads of one KV head and row run back to back on one XCD
@@ -49,13 +52,15 @@ struct FwdParams {
 
 }  // namespace
 
-template <int D>
+template <int D, int SK>
 __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(FwdParams p) {
-  constexpr int KS = D / 16;  // MFMA k-steps over the head dim
-  constexpr int DT = D / 32;  // 32-wide output column tiles
-  using U = UnitDma<D>;
-  constexpr int kUnit = U::kRows * pitch<D>();
-  __shared__ __bf16 k_lo[kUnit], k_hi[kUnit], v_lo[kUnit], v_hi[kUnit];
+  constexpr int KS = D / 16;     // MFMA k-steps over the head dim
+  constexpr int DT = D / 32;     // 32-wide output column tiles
+  constexpr int NB = SK / 32;    // 32-key blocks per step
+  constexpr int NS = kTile / SK; // steps per KV tile
+  constexpr int PK = SK / 16;    // P V k-steps per step
+  using U = UnitDma<D, kWaves, SK>;
+  __shared__ __bf16 k_a[U::kElems], k_b[U::kElems], v_a[U::kElems], v_b[U::kElems];
 
   const int b = blockIdx.z;
   const int tid = threadIdx.x, wave = uniform(tid >> 6), lane = tid & 63;
@@ -88,11 +93,11 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(FwdParams p)
   int koff[U::kPerWave + 1], voff[U::kPerWave + 1];
 #pragma unroll
   for (int j = 0; j < U::kPerWave; ++j) {
-    koff[j] = unit_dma_offset<D>(wave + kWaves * j, p.k_st, lane);
-    voff[j] = unit_dma_offset<D>(wave + kWaves * j, p.v_st, lane);
+    koff[j] = unit_dma_offset<D, SK>(wave + kWaves * j, p.k_st, lane);
+    voff[j] = unit_dma_offset<D, SK>(wave + kWaves * j, p.v_st, lane);
   }
-  koff[U::kPerWave] = unit_dma_offset<D>(U::kInsts - 1, p.k_st, lane);
-  voff[U::kPerWave] = unit_dma_offset<D>(U::kInsts - 1, p.v_st, lane);
+  koff[U::kPerWave] = unit_dma_offset<D, SK>(U::kInsts - 1, p.k_st, lane);
+  voff[U::kPerWave] = unit_dma_offset<D, SK>(U::kInsts - 1, p.v_st, lane);
 
   const size_t row = (size_t)mb * nt + qt;
   const int npart = uniform(p.m.kv_num[row]);
@@ -110,14 +115,14 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(FwdParams p)
   };
   int tiles_v = load_chunk(0);
   auto tile_of = [&](int it) { return __builtin_amdgcn_readlane(tiles_v, it & 63); };
-  // K and V rows [t0, t0 + 64) into one half's units.
+  // K and V rows [t0, t0 + SK) into one step's units.
   // (t0 >= T, e.g. past the last tile, copies zeros.)
   const auto krs = slice_rsrc(kbase, p.k_st, T, D);
   const auto vrs = slice_rsrc(vbase, p.v_st, T, D);
   const int k_row2 = (int)p.k_st * 2, v_row2 = (int)p.v_st * 2;
-  auto load_half = [&](__bf16* kd, __bf16* vd, int t0) {
-    unit_dma<D>(kd, krs, koff, t0 * k_row2, wave, 0);
-    unit_dma<D>(vd, vrs, voff, t0 * v_row2, wave, 1);
+  auto load_step = [&](__bf16* kd, __bf16* vd, int t0) {
+    unit_dma<D, kWaves, SK>(kd, krs, koff, t0 * k_row2, wave, 0);
+    unit_dma<D, kWaves, SK>(vd, vrs, voff, t0 * v_row2, wave, 1);
   };
   // The lane's four bitmap words (its query row of the tile's row-major
   // bitmap) of iteration it, loaded into registers one tile ahead.  (Tiles
@@ -135,26 +140,28 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(FwdParams p)
   for (int dt = 0; dt < DT; ++dt) oacc[dt] = f32x16{};
   float m_ref = -INFINITY, l_run = 0.f;  // reference max of raw scores, running sum
 
-  // One 64-key half: S^T = K Q^T (+ mask seed), lazy-rescaled online softmax,
-  // O^T += V^T P^T.  w0, w1: bitmap words of the half's two 32-key blocks.
-  // A half with any allowed pair is computed whole (a block without one gets
-  // an all -inf seed), which keeps each contraction one straight-line run of
-  // two interleaved accumulator chains.
-  auto half_step = [&](const __bf16* kt_lds, const __bf16* vt_lds, uint32_t w0, uint32_t w1,
-                       bool partial) {
-    if (partial && __ballot((w0 | w1) != 0u) == 0ull) return;
-    f32x16 st[2];
-    // The two chains start from the mask seeds (mixed halves) or from the
-    // MFMA's inline zero (no register initialisation): one copy of the run
-    // for each start.  MFMA runs issue at raised wave priority, so that the
-    // wave sharing the SIMD fills the gaps with its softmax instead of
-    // competing for issue.
+  // One step of SK keys (NB 32-key blocks): S^T = K Q^T (+ mask seed),
+  // lazy-rescaled online softmax, O^T += V^T P^T.  w0, w1: bitmap words of
+  // the step's 32-key blocks (w1 unused when NB = 1).  A step with any
+  // allowed pair is computed whole (a block without one gets an all -inf
+  // seed), which keeps each contraction one straight-line run of NB
+  // interleaved accumulator chains.
+  auto step = [&](const __bf16* kt_lds, const __bf16* vt_lds, uint32_t w0, uint32_t w1,
+                  bool partial) {
+    const uint32_t w_any = NB == 2 ? (w0 | w1) : w0, w_all = NB == 2 ? (w0 & w1) : w0;
+    if (partial && __ballot(w_any != 0u) == 0ull) return;
+    f32x16 st[NB];
+    // The chains start from the mask seeds (mixed steps) or from the MFMA's
+    // inline zero (no register initialisation): one copy of the run for each
+    // start.  MFMA runs issue at raised wave priority, so that the waves
+    // sharing the SIMD fill the gaps with their softmax instead of competing
+    // for issue.
     auto score_run = [&](auto seeded) __attribute__((always_inline)) {
       __builtin_amdgcn_s_setprio(1);
 #pragma unroll
       for (int s = 0; s < KS; ++s)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
+        for (int j = 0; j < NB; ++j) {
           const bf16x8 kf = lds_row8<D>(kt_lds, 32 * j + tok_perm(n), 16 * s + 8 * g);
           if (decltype(seeded)::value || s > 0)
             st[j] = mfma32(kf, qf[s], st[j]);
@@ -164,16 +171,16 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(FwdParams p)
       // Issue the K reads a few MFMAs ahead of their use.
       __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
 #pragma unroll
-      for (int i = 0; i < 2 * KS - 4; ++i) {
+      for (int i = 0; i < NB * KS - 4; ++i) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
         __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
       }
       __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
       __builtin_amdgcn_s_setprio(0);
     };
-    if (partial && __ballot((w0 & w1) != ~0u) != 0ull) {
+    if (partial && __ballot(w_all != ~0u) != 0ull) {
       st[0] = mask_bias(~(w0 >> g));
-      st[1] = mask_bias(~(w1 >> g));
+      if constexpr (NB == 2) st[NB - 1] = mask_bias(~(w1 >> g));
       score_run(std::true_type{});
     } else {
       score_run(std::false_type{});
@@ -192,7 +199,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(FwdParams p)
       const float neg = m_ref == -INFINITY ? 0.f : -m_ref * c;
       float rs = 0.f;
 #pragma unroll
-      for (int s = 0; s < 4; ++s)  // k-step s: entries [8 (s & 1), + 8) of block s >> 1
+      for (int s = 0; s < PK; ++s)  // k-step s: entries [8 (s & 1), + 8) of block s >> 1
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
           const float e = fast_exp2(fmaf(st[s >> 1][8 * (s & 1) + k], c, neg));
@@ -201,15 +208,18 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(FwdParams p)
         }
       return rs;
     };
-    bf16x8 pf[4];
+    bf16x8 pf[PK];
     float rs = probs(pf);
     // (pins the first evaluation ahead of the branch; the compiler would
     // otherwise move it into the branch's fall-through, behind the row max)
-    asm volatile("" ::"v"(pf[0]), "v"(pf[1]), "v"(pf[2]), "v"(pf[3]), "v"(rs));
+    if constexpr (PK == 4)
+      asm volatile("" ::"v"(pf[0]), "v"(pf[1]), "v"(pf[2]), "v"(pf[3]), "v"(rs));
+    else
+      asm volatile("" ::"v"(pf[0]), "v"(pf[1]), "v"(rs));
     if (__ballot(m_ref == -INFINITY || !(rs <= 128.f)) != 0ull) {
       float mx = -INFINITY;
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
+      for (int j = 0; j < NB; ++j)
 #pragma unroll
         for (int i = 0; i < 16; ++i) mx = fmaxf(mx, st[j][i]);
       mx = halves_max(mx);
@@ -229,7 +239,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(FwdParams p)
     // O^T += V^T P^T, 16 keys per k-step.
     __builtin_amdgcn_s_setprio(1);
 #pragma unroll
-    for (int s = 0; s < 4; ++s)
+    for (int s = 0; s < PK; ++s)
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) {
         const bf16x8 vf = lds_col8<D>(vt_lds, 16 * s, 32 * dt, lane);
@@ -238,7 +248,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(FwdParams p)
     // V transpose reads one k-step (DT MFMAs) ahead.
     __builtin_amdgcn_sched_group_barrier(0x100, 2 * DT, 1);
 #pragma unroll
-    for (int i = 0; i < 3 * DT; ++i) {
+    for (int i = 0; i < (PK - 1) * DT; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
       __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);
     }
@@ -250,30 +260,30 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_bf16_kernel(FwdParams p)
   uint4 mb_next = make_uint4(~0u, ~0u, ~0u, ~0u);
   if (ntiles > 0) {
     if (npart > 0) mb_next = load_bits(0, k0_next / kTile);
-    load_half(k_lo, v_lo, k0_next);
+    load_step(k_a, v_a, k0_next);
   }
   for (int it = 0; it < ntiles; ++it) {
     const bool partial = it < npart;
     const int k0 = k0_next;
-    // Keys [k0, k0 + 64): its units and bitmap have landed; the other half's
-    // units are free again.
-    dma_barrier();
     const uint4 mbits = partial ? mb_next : make_uint4(~0u, ~0u, ~0u, ~0u);
-    load_half(k_hi, v_hi, k0 + 64);
-    half_step(k_lo, v_lo, mbits.x, mbits.y, partial);
-
-    // Keys [k0 + 64, k0 + 128); the first half's units are free again.
-    dma_barrier();
-    const bool more = it + 1 < ntiles;
-    if (more) {
-      if (((it + 1) & 63) == 0) tiles_v = load_chunk((it + 1) >> 6);
-      k0_next = tile_of(it + 1) * kTile;
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      // Keys [k0 + SK s, + SK): their units (and at s = 0 the tile's bitmap
+      // words) have landed; the other buffer's units are free again.
+      dma_barrier();
+      __bf16 *kc = (s & 1) ? k_b : k_a, *vc = (s & 1) ? v_b : v_a;
+      __bf16 *kn = (s & 1) ? k_a : k_b, *vn = (s & 1) ? v_a : v_b;
+      if (s + 1 < NS) {
+        load_step(kn, vn, k0 + SK * (s + 1));
+      } else if (it + 1 < ntiles) {
+        if (((it + 1) & 63) == 0) tiles_v = load_chunk((it + 1) >> 6);
+        k0_next = tile_of(it + 1) * kTile;
+        if (it + 1 < npart) mb_next = load_bits(it + 1, k0_next / kTile);
+        load_step(kn, vn, k0_next);
+      }
+      auto word = [&](int i) { return i == 0 ? mbits.x : i == 1 ? mbits.y : i == 2 ? mbits.z : mbits.w; };
+      step(kc, vc, word(NB * s), word(NB * s + NB - 1), partial);
     }
-    if (more) {
-      if (it + 1 < npart) mb_next = load_bits(it + 1, k0_next / kTile);
-      load_half(k_lo, v_lo, k0_next);
-    }
-    half_step(k_hi, v_hi, mbits.z, mbits.w, partial);
   }
 
   if (qvalid) {
@@ -309,10 +319,13 @@ hipError_t launch_attn_fwd_bf16(const TensorView& q, const TensorView& k, const 
   p.m = mask;
   if (mask.nt == 0 || dims.B == 0 || dims.Hq == 0) return hipSuccess;
   dim3 grid(dims.Hq, mask.nt, dims.B);
+  // Keys per step: 64 at D = 64 (128 VGPRs, 36 KiB: four work-groups per
+  // CU), 32 at D = 128 (158 VGPRs, 36 KiB: three per CU, where 64-key halves
+  // hold 180 VGPRs and 68 KiB, two per CU).
   if (dims.D == 64)
-    hipLaunchKernelGGL(attn_fwd_bf16_kernel<64>, grid, dim3(kThreads), 0, stream, p);
+    hipLaunchKernelGGL((attn_fwd_bf16_kernel<64, 64>), grid, dim3(kThreads), 0, stream, p);
   else
-    hipLaunchKernelGGL(attn_fwd_bf16_kernel<128>, grid, dim3(kThreads), 0, stream, p);
+    hipLaunchKernelGGL((attn_fwd_bf16_kernel<128, 32>), grid, dim3(kThreads), 0, stream, p);
   return hipGetLastError();
 }
 

@@ -65,27 +65,33 @@ __device__ __forceinline__ constexpr int acc_tok(int i, int g) {
 }
 
 // Direct global -> LDS copies (buffer_load ... lds, no staging registers) of
-// 64 token rows into a padded LDS unit [64][D + 8].  One instruction moves 64
-// lanes x 16 bytes into 64 consecutive 16-byte LDS slots; a padded row is
-// kSlots = D / 8 + 1 slots (the last one is the pad, loaded from an offset past
-// any buffer so that it reads zero and touches no memory), so a unit is exactly
-// kSlots instructions.  Instruction i, lane l covers slot 64 i + l.
-template <int D, int NW = kWaves>
+// Rows token rows (64 or 32) into a padded LDS unit [Rows][D + 8].  One
+// instruction moves 64 lanes x 16 bytes into 64 consecutive 16-byte LDS
+// slots; a padded row is kSlots = D / 8 + 1 slots (the last one is the pad,
+// loaded from an offset past any buffer so that it reads zero and touches no
+// memory).  A 64-row unit is exactly kSlots instructions; a 32-row unit is
+// kSlots / 2 + 1 of them, the second half of its last instruction landing in
+// 32 sink slots after the rows (kElems counts them).  Instruction i, lane l
+// covers slot 64 i + l.
+template <int D, int NW = kWaves, int Rows = 64>
 struct UnitDma {
-  static constexpr int kRows = 64;
+  static constexpr int kRows = Rows;
   static constexpr int kSlots = D / 8 + 1;                 // 17 (D = 128) or 9 (D = 64)
-  static constexpr int kInsts = kSlots;                    // kRows * kSlots / 64
+  static constexpr int kInsts = (Rows * kSlots + 63) / 64; // 17 / 9 (64 rows), 9 / 5 (32 rows)
+  static constexpr int kElems = kInsts * 64 * 8;           // LDS elements, sink included
   static constexpr int kPerWave = kInsts / NW;             // + 1 for one wave
+  static_assert(Rows == 64 || Rows == 32, "64- or 32-row units");
   static_assert(kInsts % NW == 1, "one remainder instruction per unit");
 };
 
-// Per-lane byte offset of unit instruction i (relative to the unit's first row).
-template <int D>
+// Per-lane byte offset of unit instruction i (relative to the unit's first
+// row); pad and sink slots get an offset past any buffer (zero fill).
+template <int D, int Rows = 64>
 __device__ __forceinline__ int unit_dma_offset(int i, int64_t st, int lane) {
-  using U = UnitDma<D>;
+  using U = UnitDma<D, kWaves, Rows>;
   const int slot = 64 * i + lane;
   const int row = slot / U::kSlots, chunk = slot % U::kSlots;
-  return chunk < D / 8 ? (int)((row * st + chunk * 8) * 2) : 0x7ffffff0;
+  return (chunk < D / 8 && row < Rows) ? (int)((row * st + chunk * 8) * 2) : 0x7ffffff0;
 }
 
 // Wave `wave`'s share of a unit copy by NW waves: instructions wave + NW j,
@@ -96,10 +102,10 @@ __device__ __forceinline__ int unit_dma_offset(int i, int64_t st, int lane) {
 // offset of the unit's first row; it is added to the per-lane offset, whose
 // range check then zero-fills rows at or past T (the host keeps every such
 // offset below 2^31).
-template <int D, int NW = kWaves>
+template <int D, int NW = kWaves, int Rows = 64>
 __device__ __forceinline__ void unit_dma(__bf16* dst, __amdgpu_buffer_rsrc_t src, const int* voff,
                                          int row_off, int wave, int extra_wave) {
-  using U = UnitDma<D, NW>;
+  using U = UnitDma<D, NW, Rows>;
 #pragma unroll
   for (int j = 0; j < U::kPerWave; ++j)
     __builtin_amdgcn_raw_ptr_buffer_load_lds(
