@@ -129,7 +129,7 @@ def executed_work(bm, B: int, Hq: int, D: int, n_pairs: int, config: int):
 
     The kernels compute whole MFMA blocks: the forward a 32-query x SK-key
     step of a non-skip tile (SK = fwd_step_keys(D)) when any pair in it is
-    allowed (SK D / 128 MFMAs: the scores and P V), dK/dV and dQ a 32 x 32
+    allowed (SK D / 256 MFMAs: the scores and P V), dK/dV and dQ a 32 x 32
     block when any pair in it is allowed (D / 4 MFMAs: S, dP, dV, dK;
     3 D / 16: S, dP, dQ).  An MFMA
     (32 x 32 x 16) is 32768 FLOP.  Useful work is 4 D (forward), 8 D (dK/dV,
@@ -156,7 +156,7 @@ def executed_work(bm, B: int, Hq: int, D: int, n_pairs: int, config: int):
     units_fwd = words.view(-1, 4, 32, 128 // sk, sk // 32).any(4).any(2)  # [P, q blk, k step]
     n_blk = (16 * n_full + int(blocks32.sum())) * rows_per_mask * Hq
     n_fwd = (4 * (128 // sk) * n_full + int(units_fwd.sum())) * rows_per_mask * Hq
-    mf = {"attn_fwd_bf16_kernel": n_fwd * sk * D // 128,
+    mf = {"attn_fwd_bf16_kernel": n_fwd * sk * D // 256,
           dkdv: n_blk * D // 4,
           "bwd_dq_kernel": n_blk * 3 * D // 16}
     useful = {"attn_fwd_bf16_kernel": 4.0, dkdv: 8.0, "bwd_dq_kernel": 6.0}

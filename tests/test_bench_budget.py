@@ -24,13 +24,16 @@ def test_executed_work_counts_nonempty_blocks(T, words, D, Hq):
     blk = pad.reshape(nt * 4, 32, nt * 4, 32).any((1, 3)).sum()      # 32 x 32 blocks
     sk = 64 if D == 64 else 32                                        # forward step keys
     units = pad.reshape(nt * 4, 32, nt * 128 // sk, sk).any((1, 3)).sum()  # 32 queries x sk keys
+    # per step: a score MFMA per 32-key block and 16-wide k-step over D, a
+    # P V MFMA per 16-key k-step and 32-wide output column tile
+    fwd_unit = (sk // 32) * (D // 16) + (sk // 16) * (D // 32)
     ew = bench.executed_work(bm, 1, Hq, D, n_pairs, config=0)
-    assert ew["attn_fwd_bf16_kernel"]["mfma_per_launch"] == units * Hq * sk * D // 128
+    assert ew["attn_fwd_bf16_kernel"]["mfma_per_launch"] == units * Hq * fwd_unit
     assert ew[bench.dkdv_kernel_name(D)]["mfma_per_launch"] == blk * Hq * D // 4
     assert ew["bwd_dq_kernel"]["mfma_per_launch"] == blk * Hq * 3 * D // 16
     step = ew["step"]
     useful = 14 * D * n_pairs * Hq
-    executed = 32768 * (units * sk * D // 128 + blk * D // 4 + blk * 3 * D // 16) * Hq
+    executed = 32768 * (units * fwd_unit + blk * D // 4 + blk * 3 * D // 16) * Hq
     assert step["executed_over_useful"] == pytest.approx(executed / useful, abs=1e-4)
     assert step["busy_needed_for_50pct"] == pytest.approx(0.5 * executed / useful, abs=1e-4)
     assert "profile_mfma" not in ew  # no committed summary for config 0
