@@ -9,6 +9,7 @@
 //
 // It walks the same BlockMask lists and tile bitmaps as the bf16 kernel, with
 // the same per-(b, query head, 128-query tile) work-groups, 64-key halves
+// (the bf16 kernel's step at D = 64; its D = 128 form uses 32-key steps)
 // double-buffered in LDS by direct global->LDS copies (a float32 row of D
 // values is copied as a bf16 row of 2 D, so the copy units and row padding
 // are the bf16 ones: pitch D + 4 floats) and lazy-rescaled online softmax in
